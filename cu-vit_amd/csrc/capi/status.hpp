@@ -1,0 +1,51 @@
+// Status plumbing for the C ABI: the thread-local last error, and the mapping
+// from C++ exceptions (thrown by the host-side classes) to status codes.
+#pragma once
+
+#include "cuvit/capi.h"
+#include "cuvit/hip_check.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <new>
+#include <stdexcept>
+#include <string>
+
+namespace cuvit::capi {
+
+/// Records @p message as this thread's last error and returns @p status.
+int fail(cuvit_status status, const std::string& message);
+
+/// Records success and returns CUVIT_OK.
+int ok();
+
+/// Turns a launch result into a status, naming the failed call.
+int from_hip(hipError_t result, const char* what);
+
+/// Stores the hipError_t reported by cuvit_last_hip_error().
+void set_hip_error(int code);
+
+/// Runs @p body, mapping any exception it throws to the matching status.
+template <typename Body> int guarded(Body&& body) {
+    try {
+        return body();
+    } catch (const HipError& error) {
+        const int status = fail(CUVIT_ERROR_HIP, error.what());
+        set_hip_error(static_cast<int>(error.code()));
+        return status;
+    } catch (const std::invalid_argument& error) {
+        return fail(CUVIT_ERROR_INVALID_ARGUMENT, error.what());
+    } catch (const std::length_error& error) {
+        return fail(CUVIT_ERROR_LENGTH, error.what());
+    } catch (const std::out_of_range& error) {
+        return fail(CUVIT_ERROR_OUT_OF_RANGE, error.what());
+    } catch (const std::bad_alloc&) {
+        return fail(CUVIT_ERROR_RUNTIME, "host allocation failed");
+    } catch (const std::exception& error) {
+        return fail(CUVIT_ERROR_RUNTIME, error.what());
+    } catch (...) {
+        return fail(CUVIT_ERROR_RUNTIME, "unknown exception");
+    }
+}
+
+} // namespace cuvit::capi

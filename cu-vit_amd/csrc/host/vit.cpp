@@ -1,0 +1,304 @@
+// VisionTransformer: the launch sequence of the reference's forward pass
+// (src/model/vit.cu:173-317) over arena-carved activations.
+//
+// Per block (run_block, vit.cu:173-261): LN1 -> QKV GEMM -> Q.K^T GEMM (alpha
+// 1/sqrt(head_dim), split batch over (image, head)) -> softmax in place ->
+// attention.V GEMM written straight into [tokens, heads * head_dim] -> proj
+// GEMM accumulating into the residual stream -> LN2 -> FC1 GEMM with the GELU
+// epilogue -> FC2 GEMM accumulating into the residual stream.
+// Around the blocks (forward, vit.cu:263-317): patch gather -> embedding GEMM
+// into rows 1.. of each image -> class token into row 0 -> positional add ->
+// blocks -> final LN -> head GEMM on the class rows only.
+#include "cuvit/vit.hpp"
+
+#include "cuvit/hip_check.hpp"
+#include "cuvit/kernels.hpp"
+
+#include <cmath>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace cuvit {
+namespace {
+
+std::string block_prefix(int index) { return "blocks." + std::to_string(index) + '.'; }
+
+/// Carves space for @p name from @p arena and copies the (shape-checked)
+/// tensor into it.
+const float* upload(DeviceArena& arena, const WeightFile& file, const std::string& name,
+                    const std::vector<Extent>& extents) {
+    const float* const host = file.float_data(name, extents);
+    Extent count = 1;
+    for (const Extent e : extents) {
+        count *= e;
+    }
+    float* const device = arena.allocate_raw<float>(static_cast<std::size_t>(count));
+    CUVIT_HIP_CHECK(hipMemcpy(device, host, static_cast<std::size_t>(count) * sizeof(float),
+                              hipMemcpyHostToDevice));
+    return device;
+}
+
+} // namespace
+
+void VitConfig::validate() const {
+    if (image_size <= 0 || patch_size <= 0 || channels <= 0 || embed_dim <= 0 || depth <= 0 ||
+        heads <= 0 || mlp_hidden <= 0 || classes <= 0) {
+        throw std::invalid_argument("Every ViT dimension must be positive");
+    }
+    if (image_size % patch_size != 0) {
+        throw std::invalid_argument("The image size must divide into whole patches");
+    }
+    if (embed_dim % heads != 0) {
+        throw std::invalid_argument("The embedding dimension must divide across the heads");
+    }
+}
+
+std::vector<std::string> VisionTransformer::expected_tensor_names(const VitConfig& config) {
+    std::vector<std::string> names = {"cls_token", "pos_embed", "patch_embed.proj.weight",
+                                      "patch_embed.proj.bias"};
+    static const char* const kBlockTensors[] = {
+        "norm1.weight",     "norm1.bias",     "attn.qkv.weight", "attn.qkv.bias",
+        "attn.proj.weight", "attn.proj.bias", "norm2.weight",    "norm2.bias",
+        "mlp.fc1.weight",   "mlp.fc1.bias",   "mlp.fc2.weight",  "mlp.fc2.bias"};
+    for (int block = 0; block < config.depth; ++block) {
+        for (const char* suffix : kBlockTensors) {
+            names.push_back(block_prefix(block) + suffix);
+        }
+    }
+    for (const char* name : {"norm.weight", "norm.bias", "head.weight", "head.bias"}) {
+        names.emplace_back(name);
+    }
+    return names;
+}
+
+std::size_t VisionTransformer::image_elements() const noexcept {
+    return static_cast<std::size_t>(config_.channels) * config_.image_size * config_.image_size;
+}
+
+VisionTransformer::VisionTransformer(const VitConfig& config, const WeightFile& file, int max_batch)
+    : config_(config), max_batch_(max_batch) {
+    config_.validate();
+    if (max_batch_ < 1) {
+        throw std::invalid_argument("The maximum batch size must be at least one");
+    }
+
+    const Extent embed = config_.embed_dim;
+    const Extent tokens = config_.token_count();
+    const Extent patches = config_.patch_count();
+    const Extent hidden = config_.mlp_hidden;
+    const Extent patch_elements = config_.patch_elements();
+    const Extent classes = config_.classes;
+
+    // The weight arena is sized from the configuration, not from the file, so
+    // extra tensors in a file cost nothing.
+    const std::vector<Extent> per_block = {embed,         embed, 3 * embed * embed, 3 * embed,
+                                           embed * embed, embed, embed,             embed,
+                                           hidden * embed, hidden, embed * hidden,  embed};
+    std::size_t weight_bytes = 0;
+    for (const Extent count : {embed, tokens * embed, embed * patch_elements, embed}) {
+        weight_bytes += DeviceArena::reserved_bytes<float>(static_cast<std::size_t>(count));
+    }
+    for (int block = 0; block < config_.depth; ++block) {
+        for (const Extent count : per_block) {
+            weight_bytes += DeviceArena::reserved_bytes<float>(static_cast<std::size_t>(count));
+        }
+    }
+    for (const Extent count : {embed, embed, classes * embed, classes}) {
+        weight_bytes += DeviceArena::reserved_bytes<float>(static_cast<std::size_t>(count));
+    }
+    weights_.reserve(weight_bytes);
+
+    class_token_ = upload(weights_, file, "cls_token", {1, 1, embed});
+    position_embedding_ = upload(weights_, file, "pos_embed", {1, tokens, embed});
+    // The Conv2d weight [embed, C, P, P] is already the [embed, C*P*P] matrix
+    // the embedding GEMM wants.
+    patch_weight_ = upload(weights_, file, "patch_embed.proj.weight",
+                           {embed, config_.channels, config_.patch_size, config_.patch_size});
+    patch_bias_ = upload(weights_, file, "patch_embed.proj.bias", {embed});
+
+    blocks_.resize(static_cast<std::size_t>(config_.depth));
+    for (int index = 0; index < config_.depth; ++index) {
+        const std::string p = block_prefix(index);
+        BlockWeights& b = blocks_[static_cast<std::size_t>(index)];
+        b.norm1_gamma = upload(weights_, file, p + "norm1.weight", {embed});
+        b.norm1_beta = upload(weights_, file, p + "norm1.bias", {embed});
+        b.qkv_weight = upload(weights_, file, p + "attn.qkv.weight", {3 * embed, embed});
+        b.qkv_bias = upload(weights_, file, p + "attn.qkv.bias", {3 * embed});
+        b.proj_weight = upload(weights_, file, p + "attn.proj.weight", {embed, embed});
+        b.proj_bias = upload(weights_, file, p + "attn.proj.bias", {embed});
+        b.norm2_gamma = upload(weights_, file, p + "norm2.weight", {embed});
+        b.norm2_beta = upload(weights_, file, p + "norm2.bias", {embed});
+        b.fc1_weight = upload(weights_, file, p + "mlp.fc1.weight", {hidden, embed});
+        b.fc1_bias = upload(weights_, file, p + "mlp.fc1.bias", {hidden});
+        b.fc2_weight = upload(weights_, file, p + "mlp.fc2.weight", {embed, hidden});
+        b.fc2_bias = upload(weights_, file, p + "mlp.fc2.bias", {embed});
+    }
+
+    final_gamma_ = upload(weights_, file, "norm.weight", {embed});
+    final_beta_ = upload(weights_, file, "norm.bias", {embed});
+    head_weight_ = upload(weights_, file, "head.weight", {classes, embed});
+    head_bias_ = upload(weights_, file, "head.bias", {classes});
+
+    // Activation scratch for max_batch images, shared by every block.
+    const Extent images = max_batch_;
+    const Extent activation_counts[] = {
+        images * patches * patch_elements,        // patch matrix
+        images * tokens * embed,                  // residual stream
+        images * tokens * embed,                  // normalized
+        images * tokens * 3 * embed,              // packed q, k, v
+        images * config_.heads * tokens * tokens, // attention logits / weights
+        images * tokens * embed,                  // attention context
+        images * tokens * hidden,                 // MLP hidden
+    };
+    std::size_t activation_bytes = 0;
+    for (const Extent count : activation_counts) {
+        activation_bytes += DeviceArena::reserved_bytes<float>(static_cast<std::size_t>(count));
+    }
+    activations_.reserve(activation_bytes);
+    float** const slots[] = {&patches_, &tokens_, &normalized_, &qkv_, &attention_, &context_, &hidden_};
+    for (std::size_t i = 0; i < 7; ++i) {
+        *slots[i] = activations_.allocate_raw<float>(static_cast<std::size_t>(activation_counts[i]));
+    }
+}
+
+void VisionTransformer::run_block(const BlockWeights& block, float* tokens, int batch,
+                                  hipStream_t stream) {
+    const int token_count = config_.token_count();
+    const int embed = config_.embed_dim;
+    const int heads = config_.heads;
+    const int head_dim = config_.head_dim();
+    const int hidden = config_.mlp_hidden;
+    const int rows = batch * token_count;
+    const std::int64_t tokens_per_image = static_cast<std::int64_t>(token_count) * embed;
+    const std::int64_t qkv_per_image = tokens_per_image * 3;
+    const std::int64_t logits_per_head = static_cast<std::int64_t>(token_count) * token_count;
+    const int qkv_row = 3 * embed;
+
+    launch_layer_norm(tokens, block.norm1_gamma, block.norm1_beta, normalized_, rows, embed,
+                      config_.layer_norm_epsilon, stream);
+
+    // [tokens, 3, heads, head_dim] in one projection.
+    launch_gemm(normalized_, block.qkv_weight, block.qkv_bias, qkv_,
+                gemm_problem(rows, qkv_row, embed, GemmLayout::kTransposed), stream);
+
+    // Q.K^T per (image, head), read in place from the packed projection.
+    GemmProblem logits = gemm_problem(token_count, token_count, head_dim, GemmLayout::kTransposed);
+    logits.alpha = 1.0F / std::sqrt(static_cast<float>(head_dim));
+    logits.lda = qkv_row;
+    logits.ldb = qkv_row;
+    logits.ldc = token_count;
+    logits.batch.count = batch * heads;
+    logits.batch.inner = heads;
+    logits.batch.stride_a = head_dim;
+    logits.batch.stride_b = head_dim;
+    logits.batch.stride_c = logits_per_head;
+    logits.batch.outer_stride_a = qkv_per_image;
+    logits.batch.outer_stride_b = qkv_per_image;
+    logits.batch.outer_stride_c = heads * logits_per_head;
+    launch_gemm(qkv_, qkv_ + embed, nullptr, attention_, logits, stream);
+
+    launch_softmax(attention_, attention_, batch * heads * token_count, token_count, stream);
+
+    // weights.V straight into the [tokens, heads * head_dim] context layout.
+    GemmProblem context = gemm_problem(token_count, head_dim, token_count, GemmLayout::kNoTranspose);
+    context.lda = token_count;
+    context.ldb = qkv_row;
+    context.ldc = embed;
+    context.batch.count = batch * heads;
+    context.batch.inner = heads;
+    context.batch.stride_a = logits_per_head;
+    context.batch.stride_b = head_dim;
+    context.batch.stride_c = head_dim;
+    context.batch.outer_stride_a = heads * logits_per_head;
+    context.batch.outer_stride_b = qkv_per_image;
+    context.batch.outer_stride_c = tokens_per_image;
+    launch_gemm(attention_, qkv_ + 2 * embed, nullptr, context_, context, stream);
+
+    GemmProblem projection = gemm_problem(rows, embed, embed, GemmLayout::kTransposed);
+    projection.epilogue.accumulate = true;
+    launch_gemm(context_, block.proj_weight, block.proj_bias, tokens, projection, stream);
+
+    launch_layer_norm(tokens, block.norm2_gamma, block.norm2_beta, normalized_, rows, embed,
+                      config_.layer_norm_epsilon, stream);
+
+    GemmProblem fc1 = gemm_problem(rows, hidden, embed, GemmLayout::kTransposed);
+    fc1.epilogue.gelu = true;
+    launch_gemm(normalized_, block.fc1_weight, block.fc1_bias, hidden_, fc1, stream);
+
+    GemmProblem fc2 = gemm_problem(rows, embed, hidden, GemmLayout::kTransposed);
+    fc2.epilogue.accumulate = true;
+    launch_gemm(hidden_, block.fc2_weight, block.fc2_bias, tokens, fc2, stream);
+}
+
+void VisionTransformer::forward(const float* images, float* logits, int batch, hipStream_t stream) {
+    if (batch == 0) {
+        return;
+    }
+    if (batch < 0 || batch > max_batch_) {
+        throw std::invalid_argument("This model was built for at most " + std::to_string(max_batch_) +
+                                    " images, but " + std::to_string(batch) + " were given");
+    }
+    if (images == nullptr || logits == nullptr) {
+        throw std::invalid_argument("Forward pass operands cannot be null");
+    }
+
+    const int token_count = config_.token_count();
+    const int patch_count = config_.patch_count();
+    const int embed = config_.embed_dim;
+    const std::int64_t tokens_per_image = static_cast<std::int64_t>(token_count) * embed;
+
+    launch_extract_patches(images, patches_, batch, config_.channels, config_.image_size,
+                           config_.image_size, config_.patch_size, stream);
+
+    // Patch embeddings land in rows 1.. of each image; row 0 is the class token.
+    GemmProblem embedding =
+        gemm_problem(patch_count, embed, config_.patch_elements(), GemmLayout::kTransposed);
+    embedding.batch.count = batch;
+    embedding.batch.stride_a = static_cast<std::int64_t>(patch_count) * config_.patch_elements();
+    embedding.batch.stride_c = tokens_per_image;
+    launch_gemm(patches_, patch_weight_, patch_bias_, tokens_ + embed, embedding, stream);
+
+    launch_broadcast(tokens_, class_token_, embed, tokens_per_image, batch, stream);
+    launch_add_broadcast(tokens_, position_embedding_, tokens_per_image, batch, stream);
+
+    for (const BlockWeights& block : blocks_) {
+        run_block(block, tokens_, batch, stream);
+    }
+
+    launch_layer_norm(tokens_, final_gamma_, final_beta_, normalized_, batch * token_count, embed,
+                      config_.layer_norm_epsilon, stream);
+
+    // Class-token pooling: one row per image feeds the head.
+    GemmProblem head = gemm_problem(1, config_.classes, embed, GemmLayout::kTransposed);
+    head.batch.count = batch;
+    head.batch.stride_a = tokens_per_image;
+    head.batch.stride_c = config_.classes;
+    launch_gemm(normalized_, head_weight_, head_bias_, logits, head, stream);
+}
+
+std::vector<float> VisionTransformer::forward(const std::vector<float>& images) {
+    const std::size_t per_image = image_elements();
+    if (per_image == 0 || images.size() % per_image != 0) {
+        throw std::invalid_argument("The input holds " + std::to_string(images.size()) +
+                                    " elements, which is not a whole number of " +
+                                    std::to_string(per_image) + "-element images");
+    }
+    const std::size_t batch = images.size() / per_image;
+    if (batch > static_cast<std::size_t>(max_batch_)) {
+        throw std::invalid_argument("This model was built for at most " + std::to_string(max_batch_) +
+                                    " images, but " + std::to_string(batch) + " were given");
+    }
+
+    DeviceBuffer<float> device_images(images.size());
+    DeviceBuffer<float> device_logits(batch * static_cast<std::size_t>(config_.classes));
+    Stream stream;
+    device_images.copy_from_host_async(images.data(), images.size(), stream.get());
+    forward(device_images.data(), device_logits.data(), static_cast<int>(batch), stream.get());
+    std::vector<float> logits(batch * static_cast<std::size_t>(config_.classes));
+    device_logits.copy_to_host_async(logits.data(), logits.size(), stream.get());
+    stream.synchronize();
+    return logits;
+}
+
+} // namespace cuvit

@@ -1,0 +1,133 @@
+// Device-side building blocks shared by the gfx950 kernels.
+//
+// Wavefronts are 64 lanes. A DPP "row" is 16 consecutive lanes; the reductions
+// below use DPP moves inside a row and readlane across rows, so no reduction
+// touches LDS and none needs a barrier.
+//
+// Every reduction combines its operands in an order fixed by lane position,
+// and a + b == b + a holds exactly in IEEE arithmetic, so every lane receives
+// the bit-identical total. Combined with a fixed column -> lane assignment,
+// that makes a row's result independent of where the row sits in a launch,
+// which is what keeps a batched forward pass bitwise equal to single images.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace cuvit::device {
+
+constexpr int kWave = 64;
+
+// DPP control words (GFX9 encoding).
+constexpr int kDppQuadSwap1 = 0xB1;     // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kDppQuadSwap2 = 0x4E;     // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppRowHalfMirror = 0x141; // lane j of 8 <- 7 - j
+constexpr int kDppRowMirror = 0x140;     // lane j of 16 <- 15 - j
+
+template <int Control> __device__ __forceinline__ float dpp_move(float value) {
+    return __int_as_float(
+        __builtin_amdgcn_mov_dpp(__float_as_int(value), Control, 0xF, 0xF, false));
+}
+
+struct Sum {
+    __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+};
+struct Max {
+    __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+
+/// All-reduce over each group of 16 lanes. Lane i of a group first combines
+/// with i^1, then i^2, then the mirrored half and the mirrored row, so every
+/// lane of the group ends with op over all 16 inputs.
+template <typename Op> __device__ __forceinline__ float row16_allreduce(float value, Op op) {
+    value = op(value, dpp_move<kDppQuadSwap1>(value));
+    value = op(value, dpp_move<kDppQuadSwap2>(value));
+    value = op(value, dpp_move<kDppRowHalfMirror>(value));
+    value = op(value, dpp_move<kDppRowMirror>(value));
+    return value;
+}
+
+/// All-reduce over the whole wavefront: 16-lane reduction, then the four row
+/// totals combined as (r0 op r1) op (r2 op r3) in scalar registers.
+template <typename Op> __device__ __forceinline__ float wave_allreduce(float value, Op op) {
+    value = row16_allreduce(value, op);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(value), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(value), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(value), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(value), 48));
+    return op(op(r0, r1), op(r2, r3));
+}
+
+/// Lane index inside the wavefront.
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
+
+// -- bfloat16 -----------------------------------------------------------------
+
+/// Widens bf16 bits to float: the bits are the upper half of the float.
+__device__ __forceinline__ float bf16_to_float(std::uint16_t bits) {
+    return __uint_as_float(static_cast<std::uint32_t>(bits) << 16);
+}
+
+/// Rounds a float to bf16 bits, to nearest with ties to even. NaN stays NaN
+/// (a quiet bit is forced so the truncation cannot turn it into infinity).
+__device__ __forceinline__ std::uint16_t float_to_bf16(float value) {
+    const std::uint32_t bits = __float_as_uint(value);
+    if ((bits & 0x7F800000U) == 0x7F800000U && (bits & 0x007FFFFFU) != 0) {
+        return static_cast<std::uint16_t>((bits >> 16) | 0x0040U);
+    }
+    const std::uint32_t rounding = 0x7FFFU + ((bits >> 16) & 1U);
+    return static_cast<std::uint16_t>((bits + rounding) >> 16);
+}
+
+// -- 16-byte vectors ----------------------------------------------------------
+
+/// Sixteen bytes moved by one global_load_dwordx4 / global_store_dwordx4.
+struct alignas(16) Vec16 {
+    std::uint32_t w[4];
+};
+
+__device__ __forceinline__ Vec16 load16(const void* pointer) {
+    const uint4 v = *reinterpret_cast<const uint4*>(pointer);
+    return Vec16{{v.x, v.y, v.z, v.w}};
+}
+
+__device__ __forceinline__ void store16(void* pointer, const Vec16& value) {
+    *reinterpret_cast<uint4*>(pointer) = make_uint4(value.w[0], value.w[1], value.w[2], value.w[3]);
+}
+
+/// Element access for the two storage types the kernels handle. A Vec16 holds
+/// 4 fp32 or 8 bf16 values.
+template <typename T> struct Elem;
+
+template <> struct Elem<float> {
+    static constexpr int kPerVec = 4;
+    __device__ __forceinline__ static float get(const Vec16& v, int i) {
+        return __uint_as_float(v.w[i]);
+    }
+    __device__ __forceinline__ static void set(Vec16& v, int i, float x) { v.w[i] = __float_as_uint(x); }
+    __device__ __forceinline__ static float load(const float* p) { return *p; }
+    __device__ __forceinline__ static void store(float* p, float x) { *p = x; }
+};
+
+template <> struct Elem<std::uint16_t> {
+    static constexpr int kPerVec = 8;
+    __device__ __forceinline__ static float get(const Vec16& v, int i) {
+        const std::uint32_t word = v.w[i >> 1];
+        return bf16_to_float(static_cast<std::uint16_t>((i & 1) ? (word >> 16) : (word & 0xFFFFU)));
+    }
+    __device__ __forceinline__ static void set(Vec16& v, int i, float x) {
+        const std::uint32_t bits = float_to_bf16(x);
+        std::uint32_t& word = v.w[i >> 1];
+        word = (i & 1) ? ((word & 0x0000FFFFU) | (bits << 16)) : ((word & 0xFFFF0000U) | bits);
+    }
+    __device__ __forceinline__ static float load(const std::uint16_t* p) { return bf16_to_float(*p); }
+    __device__ __forceinline__ static void store(std::uint16_t* p, float x) { *p = float_to_bf16(x); }
+};
+
+/// True when @p pointer is 16-byte aligned.
+inline bool aligned16(const void* pointer) {
+    return (reinterpret_cast<std::uintptr_t>(pointer) & 15U) == 0;
+}
+
+} // namespace cuvit::device

@@ -1,0 +1,103 @@
+// Residual add and erf GELU for gfx950.
+//
+// add:  accumulator[i] += addend[i]                (normalization.cu:148-154)
+// gelu: 0.5 * x * (1 + erf(x / sqrt(2)))           (normalization.cu:138-146,
+//       the erf form of nn.GELU(approximate='none'); CPU path
+//       tests/reference/linear_algebra.hpp:120-129)
+// A single fp32 add rounds identically everywhere, so add is bit-exact against
+// the CPU. erff is ROCm's device libm (ocml).
+//
+// Both run as grid-stride loops over 16-byte vectors when the pointers are
+// aligned, with the tail (count % elements-per-vector) handled by the first
+// threads of the grid; unaligned pointers take a scalar loop.
+#include "device_common.hpp"
+#include "launch.hpp"
+
+namespace cuvit::detail {
+namespace {
+
+using namespace cuvit::device;
+
+constexpr int kBlock = 256;
+constexpr int kBlocksPerCu = 8;
+
+__device__ __forceinline__ float gelu(float x) {
+    return 0.5F * x * (1.0F + erff(x * 0.7071067811865475F));
+}
+
+__global__ __launch_bounds__(kBlock) void add_kernel(float* __restrict__ accumulator,
+                                                     const float* __restrict__ addend,
+                                                     std::int64_t count, bool vectorized) {
+    const std::int64_t stride = static_cast<std::int64_t>(gridDim.x) * kBlock;
+    const std::int64_t first = static_cast<std::int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    std::int64_t done = 0;
+    if (vectorized) {
+        const std::int64_t vectors = count / 4;
+        for (std::int64_t v = first; v < vectors; v += stride) {
+            float4 a = reinterpret_cast<float4*>(accumulator)[v];
+            const float4 b = reinterpret_cast<const float4*>(addend)[v];
+            a.x += b.x;
+            a.y += b.y;
+            a.z += b.z;
+            a.w += b.w;
+            reinterpret_cast<float4*>(accumulator)[v] = a;
+        }
+        done = vectors * 4;
+    }
+    for (std::int64_t i = done + first; i < count; i += stride) {
+        accumulator[i] += addend[i];
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void gelu_kernel(const T* __restrict__ input,
+                                                      T* __restrict__ output, std::int64_t count,
+                                                      bool vectorized) {
+    constexpr int E = Elem<T>::kPerVec;
+    const std::int64_t stride = static_cast<std::int64_t>(gridDim.x) * kBlock;
+    const std::int64_t first = static_cast<std::int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    std::int64_t done = 0;
+    if (vectorized) {
+        const std::int64_t vectors = count / E;
+        for (std::int64_t v = first; v < vectors; v += stride) {
+            const Vec16 x = load16(input + v * E);
+            Vec16 y;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                Elem<T>::set(y, e, gelu(Elem<T>::get(x, e)));
+            }
+            store16(output + v * E, y);
+        }
+        done = vectors * E;
+    }
+    for (std::int64_t i = done + first; i < count; i += stride) {
+        Elem<T>::store(output + i, gelu(Elem<T>::load(input + i)));
+    }
+}
+
+} // namespace
+
+hipError_t add_f32(float* accumulator, const float* addend, std::int64_t count,
+                   hipStream_t stream) {
+    const bool vectorized = aligned16(accumulator) && aligned16(addend);
+    const unsigned int grid = stride_grid(vectorized ? (count + 3) / 4 : count, kBlock, kBlocksPerCu);
+    add_kernel<<<grid, kBlock, 0, stream>>>(accumulator, addend, count, vectorized);
+    return hipGetLastError();
+}
+
+hipError_t gelu_f32(const float* input, float* output, std::int64_t count, hipStream_t stream) {
+    const bool vectorized = aligned16(input) && aligned16(output);
+    const unsigned int grid = stride_grid(vectorized ? (count + 3) / 4 : count, kBlock, kBlocksPerCu);
+    gelu_kernel<float><<<grid, kBlock, 0, stream>>>(input, output, count, vectorized);
+    return hipGetLastError();
+}
+
+hipError_t gelu_bf16(const std::uint16_t* input, std::uint16_t* output, std::int64_t count,
+                     hipStream_t stream) {
+    const bool vectorized = aligned16(input) && aligned16(output);
+    const unsigned int grid = stride_grid(vectorized ? (count + 7) / 8 : count, kBlock, kBlocksPerCu);
+    gelu_kernel<std::uint16_t><<<grid, kBlock, 0, stream>>>(input, output, count, vectorized);
+    return hipGetLastError();
+}
+
+} // namespace cuvit::detail

@@ -1,0 +1,76 @@
+// Internal interface between the C ABI (validation, status codes) and the
+// kernel files (grid shaping, launch). Every function here assumes its
+// arguments were already validated and returns the launch's hipError_t.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace cuvit::detail {
+
+// layer_norm.hip
+hipError_t layer_norm_f32(const float* input, const float* gamma, const float* beta, float* output,
+                          int rows, int columns, float epsilon, hipStream_t stream);
+hipError_t layer_norm_bf16(const std::uint16_t* input, const float* gamma, const float* beta,
+                           std::uint16_t* output, int rows, int columns, float epsilon,
+                           hipStream_t stream);
+
+// softmax.hip
+hipError_t softmax_f32(const float* input, float* output, int rows, int columns,
+                       hipStream_t stream);
+hipError_t softmax_bf16(const std::uint16_t* input, std::uint16_t* output, int rows, int columns,
+                        hipStream_t stream);
+
+// patches.hip. The gather is a pure permutation, so it is typed only by the
+// element size (4 for fp32, 2 for bf16).
+hipError_t extract_patches(const void* images, void* patches, int element_size, int batch,
+                           int channels, int height, int width, int patch, hipStream_t stream);
+hipError_t broadcast_f32(float* destination, const float* source, std::int64_t count,
+                         std::int64_t destination_stride, int batch, hipStream_t stream);
+hipError_t add_broadcast_f32(float* accumulator, const float* addend, std::int64_t count, int batch,
+                             hipStream_t stream);
+
+// elementwise.hip
+hipError_t add_f32(float* accumulator, const float* addend, std::int64_t count,
+                   hipStream_t stream);
+hipError_t gelu_f32(const float* input, float* output, std::int64_t count, hipStream_t stream);
+hipError_t gelu_bf16(const std::uint16_t* input, std::uint16_t* output, std::int64_t count,
+                     hipStream_t stream);
+
+// gemm.hip. Leading dimensions are already resolved (never zero) and the
+// batch is already flattened when it has a single outer group.
+struct GemmArgs {
+    int m;
+    int n;
+    int k;
+    bool transposed;
+    float alpha;
+    int lda;
+    int ldb;
+    int ldc;
+    int count;
+    std::int64_t stride_a;
+    std::int64_t stride_b;
+    std::int64_t stride_c;
+    int inner;
+    std::int64_t outer_stride_a;
+    std::int64_t outer_stride_b;
+    std::int64_t outer_stride_c;
+    bool accumulate;
+    bool gelu;
+};
+
+hipError_t gemm_f32(const float* a, const float* b, const float* bias, float* c,
+                    const GemmArgs& args, hipStream_t stream);
+hipError_t gemm_bf16(const std::uint16_t* a, const std::uint16_t* b, const float* bias,
+                     std::uint16_t* c, const GemmArgs& args, hipStream_t stream);
+
+// Device facts used to shape grids, cached per device.
+int compute_units();
+
+/// Grid size for a grid-stride kernel: enough blocks to cover @p units of work,
+/// capped so the work-item count stays far inside the 32-bit dispatch limit.
+unsigned int stride_grid(std::int64_t units, int units_per_block, int cap_per_cu);
+
+} // namespace cuvit::detail

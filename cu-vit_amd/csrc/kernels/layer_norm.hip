@@ -1,0 +1,234 @@
+// Row-wise LayerNorm for gfx950.
+//
+// Semantics follow the reference launcher (include/cuvit/kernels.hpp:101-109)
+// and its CPU path (tests/reference/linear_algebra.hpp:70-96):
+//   out[r][c] = (in[r][c] - mean) / sqrt(var + eps) * gamma[c] + beta[c]
+// with the biased variance.
+//
+// Fast path (the ViT shapes): a team of 16 or 64 lanes owns one row and keeps
+// it in registers as 16-byte vectors, so the row is read from HBM once and
+// written once; the two statistics passes run over VGPRs. A 192-wide fp32 row
+// is 16 lanes x 3 float4, four rows per wavefront.
+//
+// Numerics: deviations are taken from the row's first element (d = x - x0),
+// which is exact for values within a factor of two of x0, and the centred value
+// is kept as d - mean(d) rather than x - (x0 + mean(d)), so a large common
+// offset never has to be represented next to the small spread. This is the
+// same remedy the reference kernel applies (normalization.cu:59-70), carried
+// one rounding further.
+//
+// Generic path (odd widths, unaligned pointers, very wide rows): one wavefront
+// per row, three strided passes over the row (the second and third hit cache).
+#include "device_common.hpp"
+#include "launch.hpp"
+
+namespace cuvit::detail {
+namespace {
+
+using namespace cuvit::device;
+
+constexpr int kBlock = 256;
+constexpr int kWavesPerBlock = kBlock / kWave;
+
+template <int Lanes, typename Op> __device__ __forceinline__ float team_allreduce(float v, Op op) {
+    if constexpr (Lanes == 16) {
+        return row16_allreduce(v, op);
+    } else {
+        return wave_allreduce(v, op);
+    }
+}
+
+/// Value of lane @p source_lane broadcast to the calling lane.
+__device__ __forceinline__ float lane_broadcast(float v, int source_lane) {
+    return __int_as_float(__builtin_amdgcn_ds_bpermute(source_lane << 2, __float_as_int(v)));
+}
+
+template <typename T, int Lanes, int V>
+__global__ __launch_bounds__(kBlock) void layer_norm_vector_kernel(
+    const T* __restrict__ input, const float* __restrict__ gamma, const float* __restrict__ beta,
+    T* __restrict__ output, int rows, int columns, float epsilon) {
+    constexpr int E = Elem<T>::kPerVec;
+    constexpr int kTeams = kWave / Lanes;
+
+    const int lane = lane_id();
+    const int team = lane / Lanes;
+    const int team_lane = lane % Lanes;
+    const int vectors = columns / E;
+
+    bool valid[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        valid[j] = team_lane + Lanes * j < vectors;
+    }
+
+    const float inverse_columns = 1.0F / static_cast<float>(columns);
+    const std::int64_t groups = (static_cast<std::int64_t>(rows) + kTeams - 1) / kTeams;
+    const std::int64_t wave_count = static_cast<std::int64_t>(gridDim.x) * kWavesPerBlock;
+    const std::int64_t first_wave =
+        static_cast<std::int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
+
+    for (std::int64_t group = first_wave; group < groups; group += wave_count) {
+        const std::int64_t row = group * kTeams + team;
+        const bool row_valid = row < rows;
+        const T* const source = input + row * columns;
+
+        Vec16 raw[V];
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            raw[j] = Vec16{{0U, 0U, 0U, 0U}};
+            if (row_valid && valid[j]) {
+                raw[j] = load16(source + (team_lane + Lanes * j) * E);
+            }
+        }
+
+        // x0 lives in element 0 of the team's first lane.
+        const float x0 =
+            lane_broadcast(Elem<T>::get(raw[0], 0), (lane / Lanes) * Lanes);
+
+        float d[V][E];
+        float partial = 0.F;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                d[j][e] = valid[j] ? Elem<T>::get(raw[j], e) - x0 : 0.F;
+                partial += d[j][e];
+            }
+        }
+        const float mean_deviation = team_allreduce<Lanes>(partial, Sum{}) * inverse_columns;
+
+        float squares = 0.F;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                d[j][e] = valid[j] ? d[j][e] - mean_deviation : 0.F;
+                squares += d[j][e] * d[j][e];
+            }
+        }
+        const float variance = team_allreduce<Lanes>(squares, Sum{}) * inverse_columns;
+        const float inverse_deviation = rsqrtf(variance + epsilon);
+
+        if (row_valid) {
+            T* const destination = output + row * columns;
+#pragma unroll
+            for (int j = 0; j < V; ++j) {
+                if (valid[j]) {
+                    const int column = (team_lane + Lanes * j) * E;
+                    Vec16 result;
+#pragma unroll
+                    for (int e = 0; e < E; e += 4) {
+                        const float4 g = *reinterpret_cast<const float4*>(gamma + column + e);
+                        const float4 b = *reinterpret_cast<const float4*>(beta + column + e);
+                        Elem<T>::set(result, e, d[j][e] * inverse_deviation * g.x + b.x);
+                        Elem<T>::set(result, e + 1, d[j][e + 1] * inverse_deviation * g.y + b.y);
+                        Elem<T>::set(result, e + 2, d[j][e + 2] * inverse_deviation * g.z + b.z);
+                        Elem<T>::set(result, e + 3, d[j][e + 3] * inverse_deviation * g.w + b.w);
+                    }
+                    store16(destination + (team_lane + Lanes * j) * E, result);
+                }
+            }
+        }
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void layer_norm_generic_kernel(
+    const T* __restrict__ input, const float* __restrict__ gamma, const float* __restrict__ beta,
+    T* __restrict__ output, int rows, int columns, float epsilon) {
+    const int lane = lane_id();
+    const float inverse_columns = 1.0F / static_cast<float>(columns);
+    const std::int64_t wave_count = static_cast<std::int64_t>(gridDim.x) * kWavesPerBlock;
+
+    for (std::int64_t row = static_cast<std::int64_t>(blockIdx.x) * kWavesPerBlock +
+                            threadIdx.x / kWave;
+         row < rows; row += wave_count) {
+        const T* const source = input + row * columns;
+        const float x0 = Elem<T>::load(source);
+
+        float partial = 0.F;
+        for (int column = lane; column < columns; column += kWave) {
+            partial += Elem<T>::load(source + column) - x0;
+        }
+        const float mean_deviation = wave_allreduce(partial, Sum{}) * inverse_columns;
+
+        float squares = 0.F;
+        for (int column = lane; column < columns; column += kWave) {
+            const float centred = (Elem<T>::load(source + column) - x0) - mean_deviation;
+            squares += centred * centred;
+        }
+        const float variance = wave_allreduce(squares, Sum{}) * inverse_columns;
+        const float inverse_deviation = rsqrtf(variance + epsilon);
+
+        T* const destination = output + row * columns;
+        for (int column = lane; column < columns; column += kWave) {
+            const float centred = (Elem<T>::load(source + column) - x0) - mean_deviation;
+            Elem<T>::store(destination + column,
+                           centred * inverse_deviation * gamma[column] + beta[column]);
+        }
+    }
+}
+
+/// Waves each compute unit is given before the kernels start looping.
+constexpr int kWavesPerCu = 16;
+
+template <typename T, int Lanes, int V>
+hipError_t launch_vector(const T* input, const float* gamma, const float* beta, T* output, int rows,
+                         int columns, float epsilon, hipStream_t stream) {
+    constexpr int kTeams = kWave / Lanes;
+    const std::int64_t groups = (static_cast<std::int64_t>(rows) + kTeams - 1) / kTeams;
+    const unsigned int grid = stride_grid(groups, kWavesPerBlock, kWavesPerCu / kWavesPerBlock);
+    layer_norm_vector_kernel<T, Lanes, V>
+        <<<grid, kBlock, 0, stream>>>(input, gamma, beta, output, rows, columns, epsilon);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t dispatch(const T* input, const float* gamma, const float* beta, T* output, int rows,
+                    int columns, float epsilon, hipStream_t stream) {
+    constexpr int E = Elem<T>::kPerVec;
+    const bool vectorizable = columns % E == 0 && aligned16(input) && aligned16(output) &&
+                              aligned16(gamma) && aligned16(beta);
+    const int vectors = columns / E;
+    if (vectorizable && vectors <= 16 * 8) {
+        switch ((vectors + 15) / 16) {
+        case 1: return launch_vector<T, 16, 1>(input, gamma, beta, output, rows, columns, epsilon, stream);
+        case 2: return launch_vector<T, 16, 2>(input, gamma, beta, output, rows, columns, epsilon, stream);
+        case 3: return launch_vector<T, 16, 3>(input, gamma, beta, output, rows, columns, epsilon, stream);
+        case 4: return launch_vector<T, 16, 4>(input, gamma, beta, output, rows, columns, epsilon, stream);
+        case 5: return launch_vector<T, 16, 5>(input, gamma, beta, output, rows, columns, epsilon, stream);
+        case 6: return launch_vector<T, 16, 6>(input, gamma, beta, output, rows, columns, epsilon, stream);
+        case 7: return launch_vector<T, 16, 7>(input, gamma, beta, output, rows, columns, epsilon, stream);
+        default: return launch_vector<T, 16, 8>(input, gamma, beta, output, rows, columns, epsilon, stream);
+        }
+    }
+    if (vectorizable && vectors <= kWave * 8) {
+        switch ((vectors + kWave - 1) / kWave) {
+        case 3: return launch_vector<T, 64, 3>(input, gamma, beta, output, rows, columns, epsilon, stream);
+        case 4: return launch_vector<T, 64, 4>(input, gamma, beta, output, rows, columns, epsilon, stream);
+        case 5: return launch_vector<T, 64, 5>(input, gamma, beta, output, rows, columns, epsilon, stream);
+        case 6: return launch_vector<T, 64, 6>(input, gamma, beta, output, rows, columns, epsilon, stream);
+        case 7: return launch_vector<T, 64, 7>(input, gamma, beta, output, rows, columns, epsilon, stream);
+        default: return launch_vector<T, 64, 8>(input, gamma, beta, output, rows, columns, epsilon, stream);
+        }
+    }
+    const unsigned int grid = stride_grid(rows, kWavesPerBlock, kWavesPerCu / kWavesPerBlock);
+    layer_norm_generic_kernel<T>
+        <<<grid, kBlock, 0, stream>>>(input, gamma, beta, output, rows, columns, epsilon);
+    return hipGetLastError();
+}
+
+} // namespace
+
+hipError_t layer_norm_f32(const float* input, const float* gamma, const float* beta, float* output,
+                          int rows, int columns, float epsilon, hipStream_t stream) {
+    return dispatch<float>(input, gamma, beta, output, rows, columns, epsilon, stream);
+}
+
+hipError_t layer_norm_bf16(const std::uint16_t* input, const float* gamma, const float* beta,
+                           std::uint16_t* output, int rows, int columns, float epsilon,
+                           hipStream_t stream) {
+    return dispatch<std::uint16_t>(input, gamma, beta, output, rows, columns, epsilon, stream);
+}
+
+} // namespace cuvit::detail

@@ -1,0 +1,265 @@
+// Patch gather, class-token broadcast and positional-embedding add for gfx950.
+//
+// extract_patches (reference: include/cuvit/kernels.hpp:125-138,
+// src/kernels/normalization.cu:159-192, CPU order tests/reference/vit.hpp:65-87)
+// rewrites planar [B, C, H, W] images as [B * (H/P) * (W/P), C * P * P] patch
+// rows, channel-major inside a row:
+//   patches[(b*NP + py*NX + px) * C*P*P + c*P*P + ly*P + lx]
+//     = images[((b*C + c)*H + py*P + ly)*W + px*P + lx]
+// It is a permutation, so the kernels move opaque 16-byte vectors and the
+// result is bit-exact by construction for any element type.
+//
+// Fast path: one workgroup per (image, channel, patch-row) strip. The strip's
+// source is P whole image rows, one contiguous span of P*W elements; its
+// destination is NX patch blocks of P*P contiguous elements each. Consecutive
+// threads write consecutive 16-byte vectors of a patch block (fully coalesced
+// stores); each quad of threads reads one 16-element run of an image row, and
+// the workgroup as a whole reads every byte of its span once, so every cache
+// line fetched from HBM is consumed by the same workgroup.
+//
+// broadcast / add_broadcast (normalization.cu:194-212) are 2-D grids over
+// (slot, vector) with float4 traffic when counts and pointers allow it.
+#include "device_common.hpp"
+#include "launch.hpp"
+
+#include <type_traits>
+
+namespace cuvit::detail {
+namespace {
+
+using namespace cuvit::device;
+
+constexpr int kBlock = 256;
+
+/// @tparam ElementSize bytes per element (4 fp32, 2 bf16).
+/// @tparam PV 16-byte vectors per patch row (P = PV * 16 / ElementSize).
+template <int ElementSize, int PV>
+__global__ __launch_bounds__(kBlock) void extract_patches_strip_kernel(
+    const unsigned char* __restrict__ images, unsigned char* __restrict__ patches, int channels,
+    int height, int width, std::int64_t strips) {
+    constexpr int kVec = 16 / ElementSize;     // elements per vector
+    constexpr int kPatch = PV * kVec;          // P
+    constexpr int kChunkVectors = kPatch * PV; // vectors in one P x P block
+    using Word = Vec16;
+
+    const int patches_across = width / kPatch;
+    const int patches_down = height / kPatch;
+    const int strip_vectors = patches_across * kChunkVectors; // = P * W / kVec
+    const std::int64_t row_elements = static_cast<std::int64_t>(channels) * kPatch * kPatch;
+
+    for (std::int64_t strip = blockIdx.x; strip < strips; strip += gridDim.x) {
+        // strip = (image * channels + channel) * patches_down + patch_row
+        const std::int64_t plane = strip / patches_down; // image * channels + channel
+        const int patch_row = static_cast<int>(strip - plane * patches_down);
+        const std::int64_t image = plane / channels;
+        const int channel = static_cast<int>(plane - image * channels);
+
+        const unsigned char* const source =
+            images + ((plane * height + static_cast<std::int64_t>(patch_row) * kPatch) * width) *
+                         ElementSize;
+        const std::int64_t first_patch =
+            (image * patches_down + patch_row) * static_cast<std::int64_t>(patches_across);
+        unsigned char* const destination =
+            patches + (first_patch * row_elements + static_cast<std::int64_t>(channel) * kPatch *
+                                                        kPatch) *
+                          ElementSize;
+
+        for (int v = threadIdx.x; v < strip_vectors; v += kBlock) {
+            const int patch_column = v / kChunkVectors; // power-of-two divisor
+            const int q = v % kChunkVectors;
+            const int local_row = q / PV;
+            const int local_vector = q % PV;
+            const std::int64_t source_element =
+                static_cast<std::int64_t>(local_row) * width + patch_column * kPatch +
+                local_vector * kVec;
+            const std::int64_t destination_element =
+                static_cast<std::int64_t>(patch_column) * row_elements +
+                static_cast<std::int64_t>(q) * kVec;
+            const Word value = load16(source + source_element * ElementSize);
+            store16(destination + destination_element * ElementSize, value);
+        }
+    }
+}
+
+/// One element per iteration, any geometry and alignment.
+template <typename Word>
+__global__ __launch_bounds__(kBlock) void extract_patches_element_kernel(
+    const Word* __restrict__ images, Word* __restrict__ patches, int channels, int height,
+    int width, int patch, std::int64_t total) {
+    const std::int64_t patch_area = static_cast<std::int64_t>(patch) * patch;
+    const std::int64_t row_length = channels * patch_area;
+    const int patches_across = width / patch;
+    const int patches_per_image = (height / patch) * patches_across;
+    const std::int64_t stride = static_cast<std::int64_t>(gridDim.x) * kBlock;
+
+    for (std::int64_t index = static_cast<std::int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+         index < total; index += stride) {
+        const std::int64_t global_patch = index / row_length;
+        const std::int64_t element = index - global_patch * row_length;
+        const std::int64_t image = global_patch / patches_per_image;
+        const int patch_index = static_cast<int>(global_patch - image * patches_per_image);
+        const int channel = static_cast<int>(element / patch_area);
+        const int within = static_cast<int>(element - channel * patch_area);
+        const int local_row = within / patch;
+        const int local_column = within - local_row * patch;
+        const int patch_row = patch_index / patches_across;
+        const int patch_column = patch_index - patch_row * patches_across;
+
+        const std::int64_t source =
+            ((image * channels + channel) * height + patch_row * patch + local_row) *
+                static_cast<std::int64_t>(width) +
+            patch_column * patch + local_column;
+        patches[index] = images[source];
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void broadcast_vector_kernel(
+    float4* __restrict__ destination, const float4* __restrict__ source, std::int64_t vectors,
+    std::int64_t destination_stride_vectors, int batch) {
+    for (std::int64_t slot = blockIdx.y; slot < batch; slot += gridDim.y) {
+        float4* const target = destination + slot * destination_stride_vectors;
+        for (std::int64_t v = static_cast<std::int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+             v < vectors; v += static_cast<std::int64_t>(gridDim.x) * kBlock) {
+            target[v] = source[v];
+        }
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void broadcast_element_kernel(
+    float* __restrict__ destination, const float* __restrict__ source, std::int64_t count,
+    std::int64_t destination_stride, int batch) {
+    for (std::int64_t slot = blockIdx.y; slot < batch; slot += gridDim.y) {
+        float* const target = destination + slot * destination_stride;
+        for (std::int64_t i = static_cast<std::int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+             i < count; i += static_cast<std::int64_t>(gridDim.x) * kBlock) {
+            target[i] = source[i];
+        }
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void add_broadcast_vector_kernel(
+    float4* __restrict__ accumulator, const float4* __restrict__ addend, std::int64_t vectors,
+    int batch) {
+    for (std::int64_t v = static_cast<std::int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+         v < vectors; v += static_cast<std::int64_t>(gridDim.x) * kBlock) {
+        const float4 a = addend[v];
+        for (std::int64_t slot = blockIdx.y; slot < batch; slot += gridDim.y) {
+            float4& target = accumulator[slot * vectors + v];
+            float4 t = target;
+            t.x += a.x;
+            t.y += a.y;
+            t.z += a.z;
+            t.w += a.w;
+            target = t;
+        }
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void add_broadcast_element_kernel(
+    float* __restrict__ accumulator, const float* __restrict__ addend, std::int64_t count,
+    int batch) {
+    for (std::int64_t i = static_cast<std::int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < count;
+         i += static_cast<std::int64_t>(gridDim.x) * kBlock) {
+        const float a = addend[i];
+        for (std::int64_t slot = blockIdx.y; slot < batch; slot += gridDim.y) {
+            accumulator[slot * count + i] += a;
+        }
+    }
+}
+
+constexpr int kStripBlocksPerCu = 8;
+constexpr std::int64_t kMaxGridY = 65535;
+
+/// (x, y) grid for the slot kernels: x covers the @p units of one slot, y the
+/// slots, with x * y bounded by a few dozen blocks per compute unit. Both
+/// kernels loop over whatever the grid does not cover.
+dim3 slot_grid(std::int64_t units, int batch) {
+    const std::int64_t budget = static_cast<std::int64_t>(compute_units()) * 32;
+    std::int64_t x = (units + kBlock - 1) / kBlock;
+    x = x < budget ? x : budget;
+    std::int64_t y = budget / x;
+    y = y < batch ? y : batch;
+    y = y < kMaxGridY ? y : kMaxGridY;
+    y = y > 0 ? y : 1;
+    return dim3(static_cast<unsigned int>(x), static_cast<unsigned int>(y));
+}
+
+template <int ElementSize, int PV>
+hipError_t launch_strips(const void* images, void* patches, int batch, int channels, int height,
+                         int width, hipStream_t stream) {
+    constexpr int kPatch = PV * 16 / ElementSize;
+    const std::int64_t strips =
+        static_cast<std::int64_t>(batch) * channels * (height / kPatch);
+    const unsigned int grid = stride_grid(strips, 1, kStripBlocksPerCu);
+    extract_patches_strip_kernel<ElementSize, PV><<<grid, kBlock, 0, stream>>>(
+        static_cast<const unsigned char*>(images), static_cast<unsigned char*>(patches), channels,
+        height, width, strips);
+    return hipGetLastError();
+}
+
+template <int ElementSize>
+hipError_t dispatch_patches(const void* images, void* patches, int batch, int channels, int height,
+                            int width, int patch, hipStream_t stream) {
+    constexpr int kVec = 16 / ElementSize;
+    if (aligned16(images) && aligned16(patches) && patch % kVec == 0) {
+        switch (patch / kVec) {
+        case 1: return launch_strips<ElementSize, 1>(images, patches, batch, channels, height, width, stream);
+        case 2: return launch_strips<ElementSize, 2>(images, patches, batch, channels, height, width, stream);
+        case 4: return launch_strips<ElementSize, 4>(images, patches, batch, channels, height, width, stream);
+        case 8: return launch_strips<ElementSize, 8>(images, patches, batch, channels, height, width, stream);
+        default: break;
+        }
+    }
+    using Word = std::conditional_t<ElementSize == 4, std::uint32_t, std::uint16_t>;
+    const std::int64_t total = static_cast<std::int64_t>(batch) * channels * height * width;
+    const unsigned int grid = stride_grid(total, kBlock, 16);
+    extract_patches_element_kernel<Word><<<grid, kBlock, 0, stream>>>(
+        static_cast<const Word*>(images), static_cast<Word*>(patches), channels, height, width,
+        patch, total);
+    return hipGetLastError();
+}
+
+} // namespace
+
+hipError_t extract_patches(const void* images, void* patches, int element_size, int batch,
+                           int channels, int height, int width, int patch, hipStream_t stream) {
+    if (element_size == 4) {
+        return dispatch_patches<4>(images, patches, batch, channels, height, width, patch, stream);
+    }
+    return dispatch_patches<2>(images, patches, batch, channels, height, width, patch, stream);
+}
+
+hipError_t broadcast_f32(float* destination, const float* source, std::int64_t count,
+                         std::int64_t destination_stride, int batch, hipStream_t stream) {
+    if (count % 4 == 0 && destination_stride % 4 == 0 && aligned16(destination) &&
+        aligned16(source)) {
+        const std::int64_t vectors = count / 4;
+        const dim3 grid = slot_grid(vectors, batch);
+        broadcast_vector_kernel<<<grid, kBlock, 0, stream>>>(
+            reinterpret_cast<float4*>(destination), reinterpret_cast<const float4*>(source),
+            vectors, destination_stride / 4, batch);
+    } else {
+        const dim3 grid = slot_grid(count, batch);
+        broadcast_element_kernel<<<grid, kBlock, 0, stream>>>(destination, source, count,
+                                                              destination_stride, batch);
+    }
+    return hipGetLastError();
+}
+
+hipError_t add_broadcast_f32(float* accumulator, const float* addend, std::int64_t count, int batch,
+                             hipStream_t stream) {
+    if (count % 4 == 0 && aligned16(accumulator) && aligned16(addend)) {
+        const std::int64_t vectors = count / 4;
+        const dim3 grid = slot_grid(vectors, batch);
+        add_broadcast_vector_kernel<<<grid, kBlock, 0, stream>>>(
+            reinterpret_cast<float4*>(accumulator), reinterpret_cast<const float4*>(addend),
+            vectors, batch);
+    } else {
+        const dim3 grid = slot_grid(count, batch);
+        add_broadcast_element_kernel<<<grid, kBlock, 0, stream>>>(accumulator, addend, count,
+                                                                  batch);
+    }
+    return hipGetLastError();
+}
+
+} // namespace cuvit::detail

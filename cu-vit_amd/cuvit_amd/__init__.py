@@ -1,0 +1,429 @@
+"""Python binding of libcuvit_amd.so, the MI355X (gfx950) layer-kernel library.
+
+The library's interface is the C ABI in include/cuvit/capi.h; this module binds
+it with ctypes so tests and the benchmark can drive the HIP kernels on device
+tensors that PyTorch allocates. PyTorch provides device memory and the stream
+handle only; every computation runs in the library's own HIP kernels. There is
+no fallback: if the library is not built, loading raises.
+
+Launcher functions mirror the reference's kernels.hpp (names, argument order,
+error behaviour): an invalid argument raises InvalidArgument (a ValueError, the
+counterpart of std::invalid_argument), an oversized launch raises LengthError,
+and a failed launch raises HipError.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+__all__ = [
+    "CuvitError", "InvalidArgument", "LengthError", "HipError", "OutOfRange",
+    "GemmProblem", "VitConfig", "library", "library_path", "check", "stream_handle",
+    "gemm", "layer_norm", "softmax", "gelu", "extract_patches", "add", "add_broadcast",
+    "broadcast", "gemm_problem", "WeightWriter", "WeightFile", "VisionTransformer",
+    "NO_TRANSPOSE", "TRANSPOSED",
+]
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_DEFAULT_LIB = os.path.join(os.path.dirname(_HERE), "lib", "libcuvit_amd.so")
+
+NO_TRANSPOSE = 0
+TRANSPOSED = 1
+
+OK = 0
+ERROR_INVALID_ARGUMENT = 1
+ERROR_LENGTH = 2
+ERROR_HIP = 3
+ERROR_RUNTIME = 4
+ERROR_OUT_OF_RANGE = 5
+
+
+class CuvitError(RuntimeError):
+    """Base of the errors a C-ABI status turns into."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+
+
+class InvalidArgument(CuvitError, ValueError):
+    """CUVIT_ERROR_INVALID_ARGUMENT (std::invalid_argument in the reference)."""
+
+
+class LengthError(CuvitError):
+    """CUVIT_ERROR_LENGTH (std::length_error)."""
+
+
+class HipError(CuvitError):
+    """CUVIT_ERROR_HIP (CudaError in the reference); .hip_code is the hipError_t."""
+
+    def __init__(self, status: int, message: str, hip_code: int):
+        super().__init__(status, message)
+        self.hip_code = hip_code
+
+
+class OutOfRange(CuvitError, IndexError):
+    """CUVIT_ERROR_OUT_OF_RANGE (std::out_of_range)."""
+
+
+class GemmBatch(ctypes.Structure):
+    _fields_ = [
+        ("count", ctypes.c_int),
+        ("stride_a", ctypes.c_int64),
+        ("stride_b", ctypes.c_int64),
+        ("stride_c", ctypes.c_int64),
+        ("inner", ctypes.c_int),
+        ("outer_stride_a", ctypes.c_int64),
+        ("outer_stride_b", ctypes.c_int64),
+        ("outer_stride_c", ctypes.c_int64),
+    ]
+
+
+class GemmEpilogue(ctypes.Structure):
+    _fields_ = [("accumulate", ctypes.c_uint8), ("gelu", ctypes.c_uint8)]
+
+
+class GemmProblem(ctypes.Structure):
+    """cuvit_gemm_problem / cuvit::GemmProblem (reference kernels.hpp:74-85)."""
+
+    _fields_ = [
+        ("m", ctypes.c_int),
+        ("n", ctypes.c_int),
+        ("k", ctypes.c_int),
+        ("layout", ctypes.c_int32),
+        ("alpha", ctypes.c_float),
+        ("lda", ctypes.c_int),
+        ("ldb", ctypes.c_int),
+        ("ldc", ctypes.c_int),
+        ("batch", GemmBatch),
+        ("epilogue", GemmEpilogue),
+    ]
+
+
+class VitConfig(ctypes.Structure):
+    """cuvit_vit_config / cuvit::VitConfig (reference vit.hpp:15-35)."""
+
+    _fields_ = [
+        ("image_size", ctypes.c_int),
+        ("patch_size", ctypes.c_int),
+        ("channels", ctypes.c_int),
+        ("embed_dim", ctypes.c_int),
+        ("depth", ctypes.c_int),
+        ("heads", ctypes.c_int),
+        ("mlp_hidden", ctypes.c_int),
+        ("classes", ctypes.c_int),
+        ("layer_norm_epsilon", ctypes.c_float),
+    ]
+
+    def patches_per_side(self) -> int:
+        return self.image_size // self.patch_size
+
+    def patch_count(self) -> int:
+        return self.patches_per_side() ** 2
+
+    def token_count(self) -> int:
+        return self.patch_count() + 1
+
+    def head_dim(self) -> int:
+        return self.embed_dim // self.heads
+
+    def patch_elements(self) -> int:
+        return self.channels * self.patch_size * self.patch_size
+
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+_SIGNATURES = {
+    "cuvit_last_error": (ctypes.c_char_p, []),
+    "cuvit_last_hip_error": (_I, []),
+    "cuvit_version": (_I, []),
+    "cuvit_gemm_problem_init": (None, [ctypes.POINTER(GemmProblem), _I, _I, _I, _I]),
+    "cuvit_gemm_f32": (_I, [_P, _P, _P, _P, ctypes.POINTER(GemmProblem), _P]),
+    "cuvit_gemm_bf16": (_I, [_P, _P, _P, _P, ctypes.POINTER(GemmProblem), _P]),
+    "cuvit_layer_norm_f32": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
+    "cuvit_layer_norm_bf16": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
+    "cuvit_gelu_f32": (_I, [_P, _P, _L, _P]),
+    "cuvit_gelu_bf16": (_I, [_P, _P, _L, _P]),
+    "cuvit_softmax_f32": (_I, [_P, _P, _I, _I, _P]),
+    "cuvit_softmax_bf16": (_I, [_P, _P, _I, _I, _P]),
+    "cuvit_extract_patches_f32": (_I, [_P, _P, _I, _I, _I, _I, _I, _P]),
+    "cuvit_extract_patches_bf16": (_I, [_P, _P, _I, _I, _I, _I, _I, _P]),
+    "cuvit_add_f32": (_I, [_P, _P, _L, _P]),
+    "cuvit_add_broadcast_f32": (_I, [_P, _P, _L, _I, _P]),
+    "cuvit_broadcast_f32": (_I, [_P, _P, _L, _L, _I, _P]),
+    "cuvit_weight_writer_create": (_I, [ctypes.POINTER(_P)]),
+    "cuvit_weight_writer_add": (_I, [_P, ctypes.c_char_p, _I, ctypes.POINTER(_L), _P]),
+    "cuvit_weight_writer_write": (_I, [_P, ctypes.c_char_p]),
+    "cuvit_weight_writer_destroy": (None, [_P]),
+    "cuvit_weight_file_load": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "cuvit_weight_file_size": (_L, [_P]),
+    "cuvit_weight_file_contains": (_I, [_P, ctypes.c_char_p]),
+    "cuvit_weight_file_float_data": (_I, [_P, ctypes.c_char_p, _I, ctypes.POINTER(_L), ctypes.POINTER(_P)]),
+    "cuvit_weight_file_entry_name": (ctypes.c_char_p, [_P, _L]),
+    "cuvit_weight_file_payload_bytes": (ctypes.c_uint64, [_P]),
+    "cuvit_weight_file_destroy": (None, [_P]),
+    "cuvit_vit_config_default": (None, [ctypes.POINTER(VitConfig)]),
+    "cuvit_vit_config_validate": (_I, [ctypes.POINTER(VitConfig)]),
+    "cuvit_vit_create": (_I, [ctypes.POINTER(VitConfig), _P, _I, ctypes.POINTER(_P)]),
+    "cuvit_vit_forward": (_I, [_P, _P, _P, _I, _P]),
+    "cuvit_vit_weight_bytes": (ctypes.c_uint64, [_P]),
+    "cuvit_vit_activation_bytes": (ctypes.c_uint64, [_P]),
+    "cuvit_vit_destroy": (None, [_P]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def library_path() -> str:
+    return os.environ.get("CUVIT_AMD_LIBRARY", _DEFAULT_LIB)
+
+
+def library() -> ctypes.CDLL:
+    """The loaded libcuvit_amd.so. Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        path = library_path()
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"libcuvit_amd.so not found at {path}: build it first "
+                "(python -c 'import __graft_entry__ as g; g.build()' or make -C cu-vit_amd)")
+        lib = ctypes.CDLL(path)
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+    return _lib
+
+
+def check(status: int) -> None:
+    """Raises the exception matching a C-ABI status."""
+    if status == OK:
+        return
+    lib = library()
+    message = (lib.cuvit_last_error() or b"").decode()
+    if status == ERROR_INVALID_ARGUMENT:
+        raise InvalidArgument(status, message)
+    if status == ERROR_LENGTH:
+        raise LengthError(status, message)
+    if status == ERROR_HIP:
+        raise HipError(status, message, lib.cuvit_last_hip_error())
+    if status == ERROR_OUT_OF_RANGE:
+        raise OutOfRange(status, message)
+    raise CuvitError(status, message)
+
+
+def _ptr(x) -> Optional[int]:
+    """Device address of a torch tensor, an int address, or None (NULL)."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    return x.data_ptr()
+
+
+def stream_handle(stream=None) -> Optional[int]:
+    """hipStream_t of a torch stream (default: torch's current stream)."""
+    import torch
+
+    if stream is None:
+        if not torch.cuda.is_available():
+            return None  # host-only use: argument validation never reaches a stream
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream or None
+
+
+def _bf16(x) -> bool:
+    if x is None or isinstance(x, int):
+        return False
+    import torch
+
+    return x.dtype == torch.bfloat16
+
+
+def gemm_problem(m: int, n: int, k: int, layout: int = NO_TRANSPOSE) -> GemmProblem:
+    """The reference's gemm_problem() (kernels.hpp:89-96)."""
+    problem = GemmProblem()
+    library().cuvit_gemm_problem_init(ctypes.byref(problem), m, n, k, layout)
+    return problem
+
+
+def gemm(a, b, bias, c, problem: GemmProblem, stream=None, bf16: Optional[bool] = None) -> None:
+    fn = library().cuvit_gemm_bf16 if (bf16 if bf16 is not None else _bf16(a)) else library().cuvit_gemm_f32
+    check(fn(_ptr(a), _ptr(b), _ptr(bias), _ptr(c), ctypes.byref(problem), stream_handle(stream)))
+
+
+def layer_norm(x, gamma, beta, out, rows: int, columns: int, epsilon: float = 1.0e-6,
+               stream=None, bf16: Optional[bool] = None) -> None:
+    fn = library().cuvit_layer_norm_bf16 if (bf16 if bf16 is not None else _bf16(x)) else library().cuvit_layer_norm_f32
+    check(fn(_ptr(x), _ptr(gamma), _ptr(beta), _ptr(out), rows, columns, epsilon,
+             stream_handle(stream)))
+
+
+def softmax(x, out, rows: int, columns: int, stream=None, bf16: Optional[bool] = None) -> None:
+    fn = library().cuvit_softmax_bf16 if (bf16 if bf16 is not None else _bf16(x)) else library().cuvit_softmax_f32
+    check(fn(_ptr(x), _ptr(out), rows, columns, stream_handle(stream)))
+
+
+def gelu(x, out, count: int, stream=None, bf16: Optional[bool] = None) -> None:
+    fn = library().cuvit_gelu_bf16 if (bf16 if bf16 is not None else _bf16(x)) else library().cuvit_gelu_f32
+    check(fn(_ptr(x), _ptr(out), count, stream_handle(stream)))
+
+
+def extract_patches(images, patches, batch: int, channels: int, height: int, width: int,
+                    patch: int, stream=None, bf16: Optional[bool] = None) -> None:
+    fn = (library().cuvit_extract_patches_bf16 if (bf16 if bf16 is not None else _bf16(images))
+          else library().cuvit_extract_patches_f32)
+    check(fn(_ptr(images), _ptr(patches), batch, channels, height, width, patch,
+             stream_handle(stream)))
+
+
+def add(accumulator, addend, count: int, stream=None) -> None:
+    check(library().cuvit_add_f32(_ptr(accumulator), _ptr(addend), count, stream_handle(stream)))
+
+
+def add_broadcast(accumulator, addend, count: int, batch: int, stream=None) -> None:
+    check(library().cuvit_add_broadcast_f32(_ptr(accumulator), _ptr(addend), count, batch,
+                                            stream_handle(stream)))
+
+
+def broadcast(destination, source, count: int, destination_stride: int, batch: int,
+              stream=None) -> None:
+    check(library().cuvit_broadcast_f32(_ptr(destination), _ptr(source), count,
+                                        destination_stride, batch, stream_handle(stream)))
+
+
+class WeightWriter:
+    """WeightFileWriter (reference weights.hpp:78-92) over the C ABI."""
+
+    def __init__(self):
+        handle = ctypes.c_void_p()
+        check(library().cuvit_weight_writer_create(ctypes.byref(handle)))
+        self._handle = handle
+
+    def add(self, name: str, array) -> None:
+        import numpy as np
+
+        data = np.ascontiguousarray(array, dtype=np.float32)
+        extents = (ctypes.c_int64 * max(data.ndim, 1))(*data.shape)
+        check(library().cuvit_weight_writer_add(self._handle, name.encode(), data.ndim, extents,
+                                                data.ctypes.data))
+
+    def write(self, path: str) -> None:
+        check(library().cuvit_weight_writer_write(self._handle, os.fsencode(path)))
+
+    def close(self) -> None:
+        if getattr(self, "_handle", None):
+            library().cuvit_weight_writer_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        self.close()
+
+
+class WeightFile:
+    """WeightFile (reference weights.hpp:45-74) over the C ABI."""
+
+    def __init__(self, path: str):
+        handle = ctypes.c_void_p()
+        check(library().cuvit_weight_file_load(os.fsencode(path), ctypes.byref(handle)))
+        self._handle = handle
+
+    @property
+    def handle(self):
+        return self._handle
+
+    def __len__(self) -> int:
+        return library().cuvit_weight_file_size(self._handle)
+
+    def contains(self, name: str) -> bool:
+        return bool(library().cuvit_weight_file_contains(self._handle, name.encode()))
+
+    def names(self):
+        lib = library()
+        return [lib.cuvit_weight_file_entry_name(self._handle, i).decode() for i in range(len(self))]
+
+    def payload_bytes(self) -> int:
+        return library().cuvit_weight_file_payload_bytes(self._handle)
+
+    def float_data(self, name: str, shape):
+        import numpy as np
+
+        extents = (ctypes.c_int64 * max(len(shape), 1))(*shape)
+        pointer = ctypes.c_void_p()
+        check(library().cuvit_weight_file_float_data(self._handle, name.encode(), len(shape),
+                                                     extents, ctypes.byref(pointer)))
+        count = int(np.prod(shape)) if len(shape) else 1
+        buffer = (ctypes.c_float * count).from_address(pointer.value) if count else []
+        return np.array(np.frombuffer(buffer, dtype=np.float32, count=count)).reshape(shape)
+
+    def close(self) -> None:
+        if getattr(self, "_handle", None):
+            library().cuvit_weight_file_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        self.close()
+
+
+def default_config() -> VitConfig:
+    config = VitConfig()
+    library().cuvit_vit_config_default(ctypes.byref(config))
+    return config
+
+
+def validate_config(config: VitConfig) -> None:
+    check(library().cuvit_vit_config_validate(ctypes.byref(config)))
+
+
+class VisionTransformer:
+    """VisionTransformer (reference vit.hpp:53-120) over the C ABI."""
+
+    def __init__(self, config: VitConfig, weights: WeightFile, max_batch: int = 1):
+        handle = ctypes.c_void_p()
+        check(library().cuvit_vit_create(ctypes.byref(config), weights.handle, max_batch,
+                                         ctypes.byref(handle)))
+        self._handle = handle
+        self.config = config
+        self.max_batch = max_batch
+
+    def forward(self, images, logits, batch: int, stream=None) -> None:
+        check(library().cuvit_vit_forward(self._handle, _ptr(images), _ptr(logits), batch,
+                                          stream_handle(stream)))
+
+    def weight_bytes(self) -> int:
+        return library().cuvit_vit_weight_bytes(self._handle)
+
+    def activation_bytes(self) -> int:
+        return library().cuvit_vit_activation_bytes(self._handle)
+
+    def close(self) -> None:
+        if getattr(self, "_handle", None):
+            library().cuvit_vit_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        self.close()
+
+
+def expected_tensor_names(config: VitConfig):
+    """VisionTransformer::expected_tensor_names (reference vit.cu:49-63), with shapes."""
+    e, t, h = config.embed_dim, config.token_count(), config.mlp_hidden
+    names = [("cls_token", (1, 1, e)), ("pos_embed", (1, t, e)),
+             ("patch_embed.proj.weight", (e, config.channels, config.patch_size, config.patch_size)),
+             ("patch_embed.proj.bias", (e,))]
+    for i in range(config.depth):
+        p = f"blocks.{i}."
+        names += [(p + "norm1.weight", (e,)), (p + "norm1.bias", (e,)),
+                  (p + "attn.qkv.weight", (3 * e, e)), (p + "attn.qkv.bias", (3 * e,)),
+                  (p + "attn.proj.weight", (e, e)), (p + "attn.proj.bias", (e,)),
+                  (p + "norm2.weight", (e,)), (p + "norm2.bias", (e,)),
+                  (p + "mlp.fc1.weight", (h, e)), (p + "mlp.fc1.bias", (h,)),
+                  (p + "mlp.fc2.weight", (e, h)), (p + "mlp.fc2.bias", (e,))]
+    names += [("norm.weight", (e,)), ("norm.bias", (e,)),
+              ("head.weight", (config.classes, e)), ("head.bias", (config.classes,))]
+    return names

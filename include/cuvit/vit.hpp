@@ -1,0 +1,110 @@
+#pragma once
+
+// The model driver: the counterpart of the reference's include/cuvit/vit.hpp
+// (VitConfig 15-35, BlockWeights 38-51, VisionTransformer 53-120) and
+// src/model/vit.cu. It sequences the layer kernels of cuvit/kernels.hpp over
+// activations carved once from a DeviceArena, so a forward pass allocates
+// nothing and issues 12 * 9 + 6 launches on one stream.
+
+#include "cuvit/device_arena.hpp"
+#include "cuvit/device_buffer.hpp"
+#include "cuvit/stream.hpp"
+#include "cuvit/tensor.hpp"
+#include "cuvit/weights.hpp"
+
+#include <hip/hip_runtime_api.h>
+
+#include <string>
+#include <vector>
+
+namespace cuvit {
+
+/// Shape of a Vision Transformer; the defaults are ViT-Tiny/16 at 224x224.
+struct VitConfig {
+    int image_size = 224;
+    int patch_size = 16;
+    int channels = 3;
+    int embed_dim = 192;
+    int depth = 12;
+    int heads = 3;
+    int mlp_hidden = 768;
+    int classes = 1000;
+    float layer_norm_epsilon = 1.0e-6F;
+
+    [[nodiscard]] int patches_per_side() const { return image_size / patch_size; }
+    [[nodiscard]] int patch_count() const { return patches_per_side() * patches_per_side(); }
+    /// Patches plus the class token.
+    [[nodiscard]] int token_count() const { return patch_count() + 1; }
+    [[nodiscard]] int head_dim() const { return embed_dim / heads; }
+    [[nodiscard]] int patch_elements() const { return channels * patch_size * patch_size; }
+
+    /// Throws std::invalid_argument when the shape cannot describe a model.
+    void validate() const;
+};
+
+struct BlockWeights {
+    const float* norm1_gamma = nullptr;
+    const float* norm1_beta = nullptr;
+    const float* qkv_weight = nullptr;
+    const float* qkv_bias = nullptr;
+    const float* proj_weight = nullptr;
+    const float* proj_bias = nullptr;
+    const float* norm2_gamma = nullptr;
+    const float* norm2_beta = nullptr;
+    const float* fc1_weight = nullptr;
+    const float* fc1_bias = nullptr;
+    const float* fc2_weight = nullptr;
+    const float* fc2_bias = nullptr;
+};
+
+class VisionTransformer final {
+  public:
+    /// Uploads @p file (shape-checked against @p config, timm names) and
+    /// reserves activations for @p max_batch images.
+    VisionTransformer(const VitConfig& config, const WeightFile& file, int max_batch = 1);
+
+    /// @p batch planar images in device memory -> batch x classes logits in
+    /// device memory, queued on @p stream.
+    void forward(const float* images, float* logits, int batch, hipStream_t stream = nullptr);
+
+    /// Host-memory convenience form; synchronizes before returning.
+    [[nodiscard]] std::vector<float> forward(const std::vector<float>& images);
+
+    [[nodiscard]] const VitConfig& config() const noexcept { return config_; }
+    [[nodiscard]] int max_batch() const noexcept { return max_batch_; }
+    [[nodiscard]] std::size_t image_elements() const noexcept;
+    [[nodiscard]] std::size_t weight_bytes() const noexcept { return weights_.used(); }
+    [[nodiscard]] std::size_t activation_bytes() const noexcept { return activations_.used(); }
+
+    /// The timm tensor names this configuration expects, in load order.
+    [[nodiscard]] static std::vector<std::string> expected_tensor_names(const VitConfig& config);
+
+  private:
+    void run_block(const BlockWeights& block, float* tokens, int batch, hipStream_t stream);
+
+    VitConfig config_;
+    int max_batch_ = 1;
+
+    DeviceArena weights_;
+    DeviceArena activations_;
+
+    const float* class_token_ = nullptr;
+    const float* position_embedding_ = nullptr;
+    const float* patch_weight_ = nullptr;
+    const float* patch_bias_ = nullptr;
+    const float* final_gamma_ = nullptr;
+    const float* final_beta_ = nullptr;
+    const float* head_weight_ = nullptr;
+    const float* head_bias_ = nullptr;
+    std::vector<BlockWeights> blocks_;
+
+    float* patches_ = nullptr;
+    float* tokens_ = nullptr;
+    float* normalized_ = nullptr;
+    float* qkv_ = nullptr;
+    float* attention_ = nullptr;
+    float* context_ = nullptr;
+    float* hidden_ = nullptr;
+};
+
+} // namespace cuvit

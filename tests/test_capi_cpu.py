@@ -1,0 +1,180 @@
+"""The C-ABI boundary on the CPU: the library loads, exports every entry point
+include/cuvit/capi.h declares, mirrors the reference's struct layout, and
+validates arguments in the reference's order and wording before any HIP call
+(src/kernels/normalization.cu:224-350, src/kernels/gemm.cu:199-231). None of
+these calls reaches a kernel, so they run without a GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "cuvit", "capi.h")
+FAKE = 0x1000  # a non-null address that is never dereferenced: validation stops first
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(cuvit_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_functions()
+    assert len(names) >= 30
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_gemm_problem_layout_matches_the_reference(cuvit):
+    """cuvit_gemm_problem mirrors cuvit::GemmProblem field for field."""
+    assert ctypes.sizeof(cuvit.GemmProblem) == 104
+    assert cuvit.GemmProblem.batch.offset == 32
+    assert cuvit.GemmProblem.epilogue.offset == 96
+    p = cuvit.gemm_problem(3, 4, 5, cuvit.TRANSPOSED)
+    assert (p.m, p.n, p.k, p.layout, p.alpha, p.lda, p.ldb, p.ldc) == (3, 4, 5, 1, 1.0, 0, 0, 0)
+    assert (p.batch.count, p.batch.inner, p.epilogue.accumulate, p.epilogue.gelu) == (1, 0, 0, 0)
+
+
+def test_zero_extents_return_before_any_check(lib):
+    """normalization.cu:226-228: empty launches succeed even with null operands."""
+    assert lib.cuvit_layer_norm_f32(None, None, None, None, 0, 4, 1e-6, None) == 0
+    assert lib.cuvit_layer_norm_f32(None, None, None, None, 4, 0, 1e-6, None) == 0
+    assert lib.cuvit_softmax_f32(None, None, 0, 4, None) == 0
+    assert lib.cuvit_gelu_f32(None, None, 0, None) == 0
+    assert lib.cuvit_add_f32(None, None, 0, None) == 0
+    assert lib.cuvit_add_broadcast_f32(None, None, 0, 3, None) == 0
+    assert lib.cuvit_add_broadcast_f32(None, None, 3, 0, None) == 0
+    assert lib.cuvit_broadcast_f32(None, None, 0, 0, 3, None) == 0
+    assert lib.cuvit_extract_patches_f32(None, None, 0, -1, -1, -1, -1, None) == 0
+    assert lib.cuvit_layer_norm_bf16(None, None, None, None, 0, 4, 1e-6, None) == 0
+    assert lib.cuvit_softmax_bf16(None, None, 4, 0, None) == 0
+
+
+@pytest.mark.parametrize("call,message", [
+    (lambda l: l.cuvit_layer_norm_f32(FAKE, FAKE, FAKE, FAKE, -1, 4, 1e-6, None),
+     "Layer norm dimensions cannot be negative"),
+    (lambda l: l.cuvit_layer_norm_f32(FAKE, None, FAKE, FAKE, 2, 4, 1e-6, None),
+     "Layer norm operands cannot be null"),
+    (lambda l: l.cuvit_softmax_f32(FAKE, FAKE, 3, -2, None), "Softmax dimensions cannot be negative"),
+    (lambda l: l.cuvit_softmax_f32(None, FAKE, 3, 2, None), "Softmax operands cannot be null"),
+    (lambda l: l.cuvit_gelu_f32(FAKE, FAKE, -5, None), "GELU element count cannot be negative"),
+    (lambda l: l.cuvit_gelu_f32(None, FAKE, 4, None), "GELU operands cannot be null"),
+    (lambda l: l.cuvit_add_f32(FAKE, FAKE, -1, None), "Residual add element count cannot be negative"),
+    (lambda l: l.cuvit_add_f32(FAKE, None, 8, None), "Residual add operands cannot be null"),
+    (lambda l: l.cuvit_add_broadcast_f32(FAKE, FAKE, -1, 2, None),
+     "Broadcast add extents cannot be negative"),
+    (lambda l: l.cuvit_add_broadcast_f32(None, FAKE, 4, 2, None),
+     "Broadcast add operands cannot be null"),
+    (lambda l: l.cuvit_broadcast_f32(FAKE, FAKE, 8, 4, 2, None), "Broadcast extents are inconsistent"),
+    (lambda l: l.cuvit_broadcast_f32(FAKE, FAKE, 4, 8, -2, None), "Broadcast extents are inconsistent"),
+    (lambda l: l.cuvit_broadcast_f32(FAKE, None, 4, 8, 2, None), "Broadcast operands cannot be null"),
+    (lambda l: l.cuvit_extract_patches_f32(FAKE, FAKE, 1, 0, 16, 16, 4, None),
+     "Patch extraction dimensions must be positive"),
+    (lambda l: l.cuvit_extract_patches_f32(FAKE, FAKE, -1, 3, 16, 16, 4, None),
+     "Patch extraction dimensions must be positive"),
+    (lambda l: l.cuvit_extract_patches_f32(FAKE, FAKE, 1, 3, 18, 16, 4, None),
+     "Patch extraction needs the image to divide into whole patches"),
+    (lambda l: l.cuvit_extract_patches_f32(None, FAKE, 1, 3, 16, 16, 4, None),
+     "Patch extraction operands cannot be null"),
+    (lambda l: l.cuvit_extract_patches_bf16(FAKE, None, 2, 3, 224, 224, 16, None),
+     "Patch extraction operands cannot be null"),
+    (lambda l: l.cuvit_gelu_bf16(FAKE, None, 3, None), "GELU operands cannot be null"),
+])
+def test_invalid_arguments(cuvit, lib, call, message):
+    status = call(lib)
+    assert status == cuvit.ERROR_INVALID_ARGUMENT
+    assert lib.cuvit_last_error().decode() == message
+
+
+def test_oversized_launches_are_length_errors(cuvit, lib):
+    """normalization.cu:214-220: more than 2^31 - 1 blocks of 256 threads."""
+    huge = (1 << 31) * 256
+    for status in (lib.cuvit_gelu_f32(FAKE, FAKE, huge, None),
+                   lib.cuvit_add_f32(FAKE, FAKE, huge, None),
+                   lib.cuvit_add_broadcast_f32(FAKE, FAKE, 1 << 30, 1 << 20, None),
+                   lib.cuvit_broadcast_f32(FAKE, FAKE, 1 << 30, 1 << 30, 1 << 20, None),
+                   lib.cuvit_extract_patches_f32(FAKE, FAKE, 1 << 20, 3, 1 << 14, 1 << 14, 16, None)):
+        assert status == cuvit.ERROR_LENGTH
+        assert "grid limit" in lib.cuvit_last_error().decode()
+
+
+def gemm_status(cuvit, lib, a=FAKE, b=FAKE, c=FAKE, **fields):
+    p = cuvit.gemm_problem(fields.pop("m", 4), fields.pop("n", 4), fields.pop("k", 4),
+                           fields.pop("layout", cuvit.NO_TRANSPOSE))
+    for key, value in fields.items():
+        if key in ("count", "inner"):
+            setattr(p.batch, key, value)
+        else:
+            setattr(p, key, value)
+    return lib.cuvit_gemm_f32(a, b, None, c, ctypes.byref(p), None)
+
+
+def test_gemm_validation_order(cuvit, lib):
+    """gemm.cu:205-231, in order."""
+    assert gemm_status(cuvit, lib, a=None, b=None, c=None, m=0) == 0
+    assert gemm_status(cuvit, lib, a=None, b=None, c=None, n=0) == 0
+    assert gemm_status(cuvit, lib, a=None, b=None, c=None, count=0) == 0
+    cases = [
+        (dict(m=-1), "GEMM dimensions cannot be negative"),
+        (dict(k=-1), "GEMM dimensions cannot be negative"),
+        (dict(count=-3), "GEMM dimensions cannot be negative"),
+        (dict(count=6, inner=4), "A split GEMM batch must divide into whole inner groups"),
+        (dict(a=None), "GEMM operands cannot be null"),
+        (dict(c=None, count=6, inner=3), "GEMM operands cannot be null"),
+        (dict(lda=3), "A GEMM leading dimension is smaller than its row"),
+        (dict(ldc=3), "A GEMM leading dimension is smaller than its row"),
+        (dict(ldb=3, layout=1), "A GEMM leading dimension is smaller than its row"),
+        (dict(ldb=3, layout=0, n=5, k=2), "A GEMM leading dimension is smaller than its row"),
+        (dict(layout=7), "GEMM layout is not a GemmLayout value"),
+    ]
+    for fields, message in cases:
+        assert gemm_status(cuvit, lib, **fields) == cuvit.ERROR_INVALID_ARGUMENT, fields
+        assert lib.cuvit_last_error().decode() == message, fields
+    # the split check precedes the null check (gemm.cu:211-216)
+    assert gemm_status(cuvit, lib, a=None, count=6, inner=4) == cuvit.ERROR_INVALID_ARGUMENT
+    assert "split" in lib.cuvit_last_error().decode()
+
+
+def test_python_errors_carry_the_status(cuvit):
+    with pytest.raises(cuvit.InvalidArgument) as info:
+        cuvit.softmax(None, FAKE, 2, 2)
+    assert isinstance(info.value, ValueError)
+    assert "null" in str(info.value)
+    with pytest.raises(cuvit.LengthError):
+        cuvit.gelu(FAKE, FAKE, (1 << 31) * 256)
+
+
+def test_config_validation(cuvit):
+    """vit_test.cu:324-345 and VitConfig::validate (vit.cu:36-47)."""
+    config = cuvit.default_config()
+    assert (config.image_size, config.patch_size, config.channels, config.embed_dim,
+            config.depth, config.heads, config.mlp_hidden, config.classes) == \
+        (224, 16, 3, 192, 12, 3, 768, 1000)
+    assert abs(config.layer_norm_epsilon - 1e-6) < 1e-12
+    cuvit.validate_config(config)
+    config.embed_dim = 25
+    config.heads = 4
+    with pytest.raises(cuvit.InvalidArgument, match="divide across the heads"):
+        cuvit.validate_config(config)
+    config = cuvit.default_config()
+    config.image_size = 30
+    with pytest.raises(cuvit.InvalidArgument, match="whole patches"):
+        cuvit.validate_config(config)
+    config = cuvit.default_config()
+    config.depth = 0
+    with pytest.raises(cuvit.InvalidArgument, match="positive"):
+        cuvit.validate_config(config)
+
+
+def test_expected_tensor_names(cuvit):
+    """vit.cu:49-63: 4 + 12 * depth + 4 timm names; ViT-Tiny has 152."""
+    names = cuvit.expected_tensor_names(cuvit.default_config())
+    assert len(names) == 152
+    assert names[0][0] == "cls_token" and names[-1][0] == "head.bias"
+    assert sum(int(__import__("numpy").prod(s)) for _, s in names) == 5717416

@@ -1,0 +1,319 @@
+"""Pins the CPU oracle before anything is judged against it.
+
+1. Bit-exact against the reference's own CPU code (tests/reference/
+   linear_algebra.hpp, elementwise.hpp) compiled in place into oracle/_ref, on
+   the reference tests' seeded inputs.
+2. Independently of the reference, against what the mathematics fixes: numpy
+   float64 formulations written differently from the loops, closed forms,
+   invariants, special cases, and planted mistakes that must fail.
+3. The seeded generator against the C++ standard's mt19937_64 value and the
+   committed first-value fixtures.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+from numerics import compare_close, compare_close_scaled, require_close, require_close_scaled, require_exact
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+# -- 1. against the reference's compiled CPU code ------------------------------
+
+LN_SHAPES = [(1, 192), (197, 192), (197, 768), (3, 1), (5, 31), (2, 1024)]
+
+
+@pytest.mark.parametrize("rows,columns", LN_SHAPES)
+def test_layer_norm_bit_exact_with_reference(oracle, reference, rows, columns):
+    g = oracle.generator(rows * 101 + columns)
+    x = g.normal(rows * columns).reshape(rows, columns)
+    gamma, beta = g.normal(columns, 1.0, 0.2), g.normal(columns, 0.0, 0.2)
+    require_exact(oracle.layer_norm(x, gamma, beta, 1e-6), reference.layer_norm(x, gamma, beta, 1e-6),
+                  "layer_norm restatement")
+    big = oracle.generator(7).normal(197 * 192, 1000.0, 1.0).reshape(197, 192)
+    ones, zeros = np.ones(192, np.float32), np.zeros(192, np.float32)
+    require_exact(oracle.layer_norm(big, ones, zeros), reference.layer_norm(big, ones, zeros),
+                  "layer_norm at offset 1000")
+
+
+@pytest.mark.parametrize("rows,columns", [(1, 2), (197, 197), (4, 1), (3, 1000), (8, 33)])
+def test_softmax_bit_exact_with_reference(oracle, reference, rows, columns):
+    x = oracle.generator(rows * 17 + columns).normal(rows * columns, 0.0, 4.0).reshape(rows, columns)
+    require_exact(oracle.softmax(x), reference.softmax(x), "softmax restatement")
+
+
+def test_gelu_bit_exact_with_reference(oracle, reference):
+    x = oracle.generator(31).normal(4099, 0.0, 3.0)
+    x[:13] = [-30, -8, -2.7, -2, -1, -0.5, 0, 0.5, 1, 2, 2.7, 8, 30]
+    require_exact(oracle.gelu(x), reference.gelu(x), "gelu restatement")
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (17, 33, 7), (65, 65, 65), (197, 64, 197),
+                                   (1, 1000, 192), (32, 48, 16)])
+@pytest.mark.parametrize("alpha", [1.0, 0.125, -2.5])
+def test_gemm_bit_exact_with_reference(oracle, reference, m, n, k, alpha):
+    g = oracle.generator(m * 31 + n * 7 + k)
+    a, b, bias = g.normal(m * k), g.normal(k * n), g.normal(n)
+    for with_bias in (None, bias):
+        require_exact(oracle.gemm(a, b, with_bias, m, n, k, alpha),
+                      reference.gemm(a, b, with_bias, m, n, k, alpha), "gemm restatement")
+        require_exact(oracle.gemm_transposed(a, b, with_bias, m, n, k, alpha),
+                      reference.gemm_transposed(a, b, with_bias, m, n, k, alpha),
+                      "gemm_transposed restatement")
+    for transposed in (False, True):
+        require_exact(oracle.term_magnitudes(a, b, m, n, k, transposed, alpha),
+                      reference.term_magnitudes(a, b, m, n, k, transposed, alpha),
+                      "term magnitudes restatement")
+
+
+def test_add_bit_exact_with_reference(oracle, reference):
+    g = oracle.generator(9)
+    left, right = g.normal(1024), g.normal(1024)
+    require_exact(oracle.add(left.copy(), right), reference.vector_add(left, right), "add")
+
+
+# -- 2. independent pins --------------------------------------------------------
+
+def numpy_layer_norm(x, gamma, beta, eps):
+    x64 = x.astype(np.float64)
+    mean = x64.mean(axis=1, keepdims=True)
+    var = x64.var(axis=1, keepdims=True)
+    return (x64 - mean) / np.sqrt(var + eps) * gamma + beta
+
+
+def test_layer_norm_against_numpy_and_invariants(oracle):
+    g = oracle.generator(11)
+    x = g.normal(33 * 192, 2.0, 3.0).reshape(33, 192)
+    gamma, beta = g.normal(192, 1.0, 0.2), g.normal(192, 0.0, 0.2)
+    out = oracle.layer_norm(x, gamma, beta, 1e-6)
+    require_close(out, numpy_layer_norm(x, gamma, beta, 1e-6), "numpy layer norm", 1e-6, 1e-6)
+    # a planted mistake (sample instead of population variance) must fail
+    x64 = x.astype(np.float64)
+    wrong = (x64 - x64.mean(1, keepdims=True)) / np.sqrt(x64.var(1, ddof=1, keepdims=True) + 1e-6) * gamma + beta
+    assert not compare_close(out, wrong, 1e-5, 1e-6)
+    # gamma scales and beta shifts: mean beta0, std gamma0 with constant affine
+    scaled = oracle.layer_norm(x, np.full(192, 2.0, np.float32), np.full(192, 0.5, np.float32), 1e-6)
+    assert np.allclose(scaled.mean(1), 0.5, atol=1e-5)
+    assert np.allclose(scaled.astype(np.float64).std(1), 2.0, atol=1e-4)
+    # a single column normalizes to beta
+    require_exact(oracle.layer_norm(np.array([[5.0], [-7.0]], np.float32), np.array([3.0], np.float32),
+                                    np.array([0.25], np.float32), 1e-6),
+                  np.full((2, 1), 0.25, np.float32), "one-column layer norm")
+
+
+def test_softmax_against_numpy_and_invariants(oracle):
+    x = oracle.generator(12).normal(40 * 197, 0.0, 4.0).reshape(40, 197)
+    out = oracle.softmax(x)
+    x64 = x.astype(np.float64)
+    e = np.exp(x64 - x64.max(1, keepdims=True))
+    require_close(out, e / e.sum(1, keepdims=True), "numpy softmax", 1e-6, 1e-9)
+    assert np.abs(out.astype(np.float64).sum(1) - 1).max() < 1e-6
+    one_hot = np.full((4, 64), -500.0, np.float32)
+    one_hot[np.arange(4), np.arange(4)] = 500.0
+    require_exact(oracle.softmax(one_hot), np.eye(4, 64, dtype=np.float32), "saturated softmax")
+    require_exact(oracle.softmax(np.array([[3.0], [-9.0]], np.float32)),
+                  np.ones((2, 1), np.float32), "one-column softmax")
+    # invariance to a constant shift of the row (within rounding)
+    require_close(oracle.softmax(x + 10.0), out, "shifted softmax", 1e-5, 1e-7)
+
+
+def test_gelu_closed_form_and_identity(oracle):
+    for v in (-30.0, -8.0, -2.7, -2.0, -1.0, -0.5, 0.0, 0.5, 1.0, 2.0, 2.7, 8.0, 30.0):
+        exact = 0.5 * v * (1.0 + math.erf(v / math.sqrt(2.0)))
+        assert abs(oracle.gelu_scalar(v) - exact) <= 1e-6 + 1e-6 * abs(exact), v
+    assert oracle.gelu_scalar(0.0) == 0.0
+    # GELU(x) - GELU(-x) = x for the erf form (Phi(x) + Phi(-x) = 1)
+    x = oracle.generator(13).normal(2000, 0.0, 3.0)
+    diff = oracle.gelu(x).astype(np.float64) - oracle.gelu(-x).astype(np.float64)
+    assert np.abs(diff - x).max() < 1e-5
+    # the tanh form is a different function at -2.7 (elementwise_test.cu:51-60)
+    p = -2.7
+    tanh_form = 0.5 * p * (1 + math.tanh(0.7978845608 * (p + 0.044715 * p ** 3)))
+    assert abs(tanh_form - oracle.gelu_scalar(p)) > 4e-4
+
+
+def test_gemm_against_numpy(oracle):
+    m, n, k = 37, 29, 53
+    g = oracle.generator(14)
+    a, b, bias = g.normal(m * k), g.normal(k * n), g.normal(n)
+    expected = (a.reshape(m, k).astype(np.float64) @ b.reshape(k, n).astype(np.float64)) * 0.5 + bias
+    scale = oracle.term_magnitudes(a, b, m, n, k, False, 0.5)
+    require_close_scaled(oracle.gemm(a, b, bias, m, n, k, 0.5), expected, scale, "numpy gemm")
+    bt = np.ascontiguousarray(b.reshape(k, n).T)
+    require_exact(oracle.gemm_transposed(a, bt, bias, m, n, k, 0.5), oracle.gemm(a, b, bias, m, n, k, 0.5),
+                  "transposed layout of the same matrix")
+    eye = np.eye(k, dtype=np.float32)
+    require_exact(oracle.gemm(a, eye, None, m, k, k), a.reshape(m, k), "identity product")
+    assert not compare_close_scaled(oracle.gemm(a, b, bias, m, n, k, 0.5),
+                                    expected - bias, scale, 1e-6, 1e-6)  # dropped bias must fail
+
+
+def test_gemm_problem_reduces_to_plain_gemm(oracle):
+    """Batch addressing and the epilogue, against per-entry plain GEMMs."""
+    images, heads, tokens, hd = 2, 3, 11, 4
+    embed = heads * hd
+    row = 3 * embed
+    qkv = oracle.generator(15).normal(images * tokens * row)
+    out = np.zeros(images * heads * tokens * tokens, np.float32)
+    oracle.gemm_problem_run(qkv, qkv[embed:], None, out, m=tokens, n=tokens, k=hd, layout=1,
+                            alpha=0.5, lda=row, ldb=row, ldc=tokens, count=images * heads, inner=heads,
+                            stride_a=hd, stride_b=hd, stride_c=tokens * tokens,
+                            outer_stride_a=tokens * row, outer_stride_b=tokens * row,
+                            outer_stride_c=heads * tokens * tokens)
+    q3 = qkv.reshape(images, tokens, 3, heads, hd)
+    for i in range(images):
+        for h in range(heads):
+            qh = np.ascontiguousarray(q3[i, :, 0, h, :])
+            kh = np.ascontiguousarray(q3[i, :, 1, h, :])
+            start = (i * heads + h) * tokens * tokens
+            require_exact(out[start:start + tokens * tokens].reshape(tokens, tokens),
+                          oracle.gemm_transposed(qh, kh, None, tokens, tokens, hd, 0.5),
+                          "split batch entry")
+    # epilogue: K = 0 gives the bias; accumulate adds; GELU after the bias
+    bias = oracle.generator(16).normal(5)
+    c = np.full(15, 9.0, np.float32)
+    oracle.gemm_problem_run(np.zeros(1, np.float32), np.zeros(1, np.float32), bias, c, m=3, n=5, k=0)
+    require_exact(c.reshape(3, 5), np.tile(bias, (3, 1)), "zero-K bias")
+    a, b = oracle.generator(17).normal(3 * 4), oracle.generator(18).normal(4 * 5)
+    existing = oracle.generator(19).normal(15)
+    c = existing.copy()
+    oracle.gemm_problem_run(a, b, bias, c, m=3, n=5, k=4, accumulate=1, gelu=1)
+    require_exact(c, existing + oracle.gelu(oracle.gemm(a, b, bias, 3, 5, 4)).reshape(-1),
+                  "accumulate after GELU after bias")
+
+
+def test_extract_patches_is_the_reshape_transpose(oracle):
+    """The gather equals an independent numpy formulation and is a permutation."""
+    for batch, channels, size, patch in ((3, 3, 32, 8), (2, 3, 224, 16), (1, 2, 12, 3)):
+        images = np.arange(batch * channels * size * size, dtype=np.float32)
+        out = oracle.extract_patches(images, batch, channels, size, size, patch)
+        n = size // patch
+        expected = images.reshape(batch, channels, n, patch, n, patch).transpose(0, 2, 4, 1, 3, 5)
+        require_exact(out, expected.reshape(batch * n * n, channels * patch * patch), "gather")
+        require_exact(np.sort(out.reshape(-1)), images, "permutation")
+
+
+def test_broadcasts_closed_form(oracle):
+    dst = oracle.generator(20).normal(3 * 10)
+    src = oracle.generator(21).normal(4)
+    expected = dst.copy().reshape(3, 10)
+    expected[:, :4] = src
+    require_exact(oracle.broadcast(dst.copy(), src, 4, 10, 3), expected.reshape(-1), "broadcast")
+    acc = oracle.generator(22).normal(3 * 6)
+    add = oracle.generator(23).normal(6)
+    require_exact(oracle.add_broadcast(acc.copy(), add, 6, 3), (acc.reshape(3, 6) + add).reshape(-1),
+                  "add_broadcast")
+
+
+def numpy_vit(config, tensors, image):
+    """tests/reference/vit.hpp:57-206 written with numpy array operations (float64)."""
+    t = [np.asarray(v, np.float64) for v in tensors]
+    e, p, c, s = config.embed_dim, config.patch_size, config.channels, config.image_size
+    n = s // p
+    heads, hd = config.heads, config.embed_dim // config.heads
+    img = np.asarray(image, np.float64).reshape(c, n, p, n, p).transpose(1, 3, 0, 2, 4)
+    patches = img.reshape(n * n, c * p * p)
+    x = np.concatenate([t[0].reshape(1, e), patches @ t[2].reshape(e, -1).T + t[3]]) + t[1].reshape(-1, e)
+
+    def ln(v, g, b):
+        mu = v.mean(1, keepdims=True)
+        return (v - mu) / np.sqrt(v.var(1, keepdims=True) + config.layer_norm_epsilon) * g + b
+
+    for blk in range(config.depth):
+        w = t[4 + 12 * blk: 16 + 12 * blk]
+        h = ln(x, w[0], w[1])
+        qkv = (h @ w[2].T + w[3]).reshape(-1, 3, heads, hd)
+        q, k, v = qkv[:, 0].transpose(1, 0, 2), qkv[:, 1].transpose(1, 0, 2), qkv[:, 2].transpose(1, 0, 2)
+        logits = q @ k.transpose(0, 2, 1) / math.sqrt(hd)
+        att = np.exp(logits - logits.max(-1, keepdims=True))
+        att /= att.sum(-1, keepdims=True)
+        ctx = (att @ v).transpose(1, 0, 2).reshape(-1, e)
+        x = x + ctx @ w[4].T + w[5]
+        h = ln(x, w[6], w[7])
+        z = h @ w[8].T + w[9]
+        z = 0.5 * z * (1 + np.vectorize(math.erf)(z / math.sqrt(2)))
+        x = x + z @ w[10].T + w[11]
+    tail = t[4 + 12 * config.depth:]
+    cls = ln(x[:1], tail[0], tail[1])
+    return (cls @ tail[2].T + tail[3])[0]
+
+
+def test_vit_forward_against_numpy(cuvit, oracle):
+    from vit_support import random_image, random_weights, small_config
+
+    config = small_config(cuvit)
+    tensors = [v for _, v in random_weights(cuvit, oracle, config, 1234)]
+    for seed in (1, 2):
+        image = random_image(oracle, config, seed)
+        require_close(oracle.vit_forward(config, tensors, image), numpy_vit(config, tensors, image),
+                      "oracle ViT vs numpy ViT", 1e-4, 1e-4)
+
+
+def test_round_bf16_matches_torch_and_special_values(oracle):
+    import torch
+
+    x = np.concatenate([oracle.generator(24).normal(5000, 0.0, 10.0),
+                        np.array([1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -0.0, 3.0e38,
+                                  np.finfo(np.float32).max, np.inf, -np.inf, 1e-40], np.float32)])
+    bits = oracle.round_bf16(x)
+    expected = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    require_exact(bits, expected, "bf16 rounding differs from torch's round-to-nearest-even")
+    assert bits[5000] == 0x3F80 and bits[5001] == 0x3F80 and bits[5002] == 0x3F82
+    nan_bits = oracle.round_bf16(np.array([np.nan], np.float32))[0]
+    assert (nan_bits & 0x7F80) == 0x7F80 and (nan_bits & 0x7F) != 0
+
+
+# -- 3. the seeded generator ----------------------------------------------------
+
+def test_mt19937_64_standard_value(oracle):
+    """[rand.predef]: the 10000th invocation of a default-constructed
+    mt19937_64 (seed 5489) yields 9981545732273789042."""
+    g = oracle.generator(5489)
+    for _ in range(9999):
+        g.raw()
+    assert g.raw() == 9981545732273789042
+
+
+def test_generator_reproducible_bounded_and_distributed(oracle):
+    """numerics_test.cu:574-599, plus the moments of each distribution."""
+    a, b = oracle.generator(1234).normal(256), oracle.generator(1234).normal(256)
+    require_exact(a, b, "the same seed produced different data")
+    assert not np.array_equal(a, oracle.generator(5678).normal(256))
+    u = oracle.generator(99).uniform(4096, -2.0, 3.0)
+    assert ((u >= -2.0) & (u <= 3.0)).all()
+    big = oracle.generator(7).normal(200000, 1.0, 0.5)
+    assert abs(big.mean() - 1.0) < 0.01 and abs(big.std() - 0.5) < 0.01
+    uu = oracle.generator(8).uniform(200000, -1.0, 1.0)
+    assert abs(uu.mean()) < 0.01 and abs(uu.var() - 1.0 / 3.0) < 0.01
+
+
+def test_generator_matches_committed_streams(oracle):
+    """The first values of every seeded stream the configurations use, as
+    written by tests/golden/make_golden.py."""
+    streams = json.load(open(os.path.join(GOLDEN, "generator_streams.json")))
+    for stream in streams:
+        g = oracle.generator(stream["seed"])
+        if stream["kind"] == "normal":
+            values = g.normal(len(stream["bits"]), stream["a"], stream["b"])
+        else:
+            values = g.uniform(len(stream["bits"]), stream["a"], stream["b"])
+        assert values.view(np.uint32).tolist() == stream["bits"], stream["label"]
+
+
+def test_reference_golden_vectors(oracle):
+    """LN / softmax / GELU outputs the reference's own CPU code produced
+    (tests/golden/reference_vectors.npz), reproduced bit for bit."""
+    data = np.load(os.path.join(GOLDEN, "reference_vectors.npz"), allow_pickle=False)
+    for width in (192, 197, 768):
+        x, g, b = data[f"ln_x_{width}"], data[f"ln_gamma_{width}"], data[f"ln_beta_{width}"]
+        require_exact(oracle.layer_norm(x, g, b, 1e-6), data[f"ln_y_{width}"], f"LN {width}")
+        require_exact(oracle.softmax(data[f"sm_x_{width}"]), data[f"sm_y_{width}"], f"softmax {width}")
+    require_exact(oracle.gelu(data["gelu_x"]), data["gelu_y"], "GELU landmarks")
+    require_exact(oracle.gemm_transposed(data["gemm_a"], data["gemm_b"], data["gemm_bias"], 9, 13, 21),
+                  data["gemm_c"], "GEMM")
