@@ -1,0 +1,281 @@
+"""Achieved HBM bandwidth of the layer-kernel path at ViT-Tiny batch 32.
+
+One step is one pass of the path over one batch:
+  LayerNorm      x[6304, 192] -> y            (32 images x 197 tokens, fp32)
+  softmax        logits[32*3*197, 197], in place, as the model runs it
+  patch gather   images[32, 3, 224, 224] -> patches[6272, 768]
+  class token    cls[192] -> row 0 of each image's tokens[32, 197, 192]
+  positional add tokens[32, 197, 192] += pos[197, 192]
+
+Inputs are synthetic (seeded device RNG), resident in HBM before timing.
+Every kernel cycles through its own pool of buffer sets larger than twice the
+256 MB Infinity Cache, so each launch reads and writes cold HBM.
+
+value        algorithmic bytes of one step / measured time of one step (GB/s);
+             the K timed steps are one captured HIP graph, timed with HIP events
+             on the stream it runs on.
+roofline     the kernel with the largest share of the step: algorithmic bytes of
+             one launch / its average launch duration, from HIP events around
+             a graph of back-to-back launches of that kernel over its pool.
+cpu_baseline the CPU oracle (a restatement of the reference's CPU loops) on a
+             bounded sample of the same workload, one core.
+
+Modes: --mode bench (default) prints the JSON line; --mode counters runs a plain
+device copy of known size and then each kernel over cold buffers, for
+rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) to read.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "cu-vit_amd"))
+
+BATCH = 32
+CHANNELS, IMAGE, PATCH = 3, 224, 16
+EMBED, HEADS = 192, 3
+TOKENS = (IMAGE // PATCH) ** 2 + 1
+PATCHES = (IMAGE // PATCH) ** 2
+ROWS = BATCH * TOKENS                 # 6304 token rows
+SOFTMAX_ROWS = BATCH * HEADS * TOKENS  # 18912 logit rows
+PATCH_ELEMENTS = CHANNELS * PATCH * PATCH
+F32 = 4
+
+# Algorithmic bytes per launch: unique bytes read plus written.
+BYTES = {
+    "layer_norm": ROWS * EMBED * 2 * F32 + 2 * EMBED * F32,
+    "softmax": SOFTMAX_ROWS * TOKENS * 2 * F32,
+    "extract_patches": BATCH * CHANNELS * IMAGE * IMAGE * 2 * F32,
+    "broadcast": BATCH * EMBED * F32 + EMBED * F32,
+    "add_broadcast": BATCH * TOKENS * EMBED * 2 * F32 + TOKENS * EMBED * F32,
+}
+STEP_BYTES = sum(BYTES.values())
+HBM_PEAK_GBS = 8000.0
+POOL_BYTES = 640 << 20  # per kernel: > 2x the 256 MB Infinity Cache
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--mode", choices=("bench", "counters"), default="bench")
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="bound on the CPU baseline's measured work")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    return p.parse_args()
+
+
+class Pools:
+    """Rotating buffer sets, one pool per kernel, each > POOL_BYTES."""
+
+    def __init__(self, torch, device):
+        def sets(per_set_bytes):
+            return max(2, -(-POOL_BYTES // per_set_bytes))
+
+        gen = torch.Generator(device=device)
+        gen.manual_seed(101)
+        self.ln_sets = sets(BYTES["layer_norm"])
+        self.ln_x = [torch.randn(ROWS * EMBED, device=device, generator=gen) for _ in range(self.ln_sets)]
+        self.ln_y = [torch.empty(ROWS * EMBED, device=device) for _ in range(self.ln_sets)]
+        self.gamma = 1.0 + 0.02 * torch.randn(EMBED, device=device, generator=gen)
+        self.beta = 0.02 * torch.randn(EMBED, device=device, generator=gen)
+        gen.manual_seed(202)
+        self.sm_sets = sets(BYTES["softmax"])
+        self.logits = [torch.randn(SOFTMAX_ROWS * TOKENS, device=device, generator=gen)
+                       for _ in range(self.sm_sets)]
+        gen.manual_seed(303)
+        self.px_sets = sets(BYTES["extract_patches"])
+        self.images = [torch.rand(BATCH * CHANNELS * IMAGE * IMAGE, device=device, generator=gen) * 2 - 1
+                       for _ in range(self.px_sets)]
+        self.patches = [torch.empty(BATCH * PATCHES * PATCH_ELEMENTS, device=device)
+                        for _ in range(self.px_sets)]
+        self.tok_sets = sets(BYTES["add_broadcast"])
+        self.tokens = [torch.randn(BATCH * TOKENS * EMBED, device=device, generator=gen)
+                       for _ in range(self.tok_sets)]
+        self.pos = 0.02 * torch.randn(TOKENS * EMBED, device=device, generator=gen)
+        self.cls = 0.02 * torch.randn(EMBED, device=device, generator=gen)
+
+    def launchers(self, cuvit):
+        """name -> function(set_index) that enqueues one launch on the current stream."""
+        return {
+            "layer_norm": lambda i: cuvit.layer_norm(
+                self.ln_x[i % self.ln_sets], self.gamma, self.beta, self.ln_y[i % self.ln_sets],
+                ROWS, EMBED, 1e-6),
+            "softmax": lambda i: cuvit.softmax(
+                self.logits[i % self.sm_sets], self.logits[i % self.sm_sets], SOFTMAX_ROWS, TOKENS),
+            "extract_patches": lambda i: cuvit.extract_patches(
+                self.images[i % self.px_sets], self.patches[i % self.px_sets], BATCH, CHANNELS,
+                IMAGE, IMAGE, PATCH),
+            "broadcast": lambda i: cuvit.broadcast(
+                self.tokens[i % self.tok_sets], self.cls, EMBED, TOKENS * EMBED, BATCH),
+            "add_broadcast": lambda i: cuvit.add_broadcast(
+                self.tokens[i % self.tok_sets], self.pos, TOKENS * EMBED, BATCH),
+        }
+
+
+def step(launch, i):
+    for name in ("extract_patches", "broadcast", "add_broadcast", "layer_norm", "softmax"):
+        launch[name](i)
+
+
+def timed_graph(torch, body, replays: int) -> float:
+    """Captures @p body into a HIP graph, replays it once untimed, then times
+    @p replays replays with HIP events on the replay stream. Returns ms per replay."""
+    graph = torch.cuda.CUDAGraph()
+    capture_stream = torch.cuda.Stream()
+    capture_stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(capture_stream):
+        with torch.cuda.graph(graph, stream=capture_stream):
+            body()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / replays
+
+
+def cpu_baseline(seconds: float):
+    """The CPU oracle over the same workload, one core, until @p seconds of
+    measured work (at least one full step)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    from oracle import Oracle
+
+    oracle = Oracle()
+    g = oracle.generator(101)
+    x = g.normal(ROWS * EMBED).reshape(ROWS, EMBED)
+    gamma, beta = g.normal(EMBED, 1.0, 0.02), g.normal(EMBED, 0.0, 0.02)
+    logits = oracle.generator(202).normal(SOFTMAX_ROWS * TOKENS).reshape(SOFTMAX_ROWS, TOKENS)
+    g = oracle.generator(303)
+    images = g.uniform(BATCH * CHANNELS * IMAGE * IMAGE)
+    pos, cls = g.normal(TOKENS * EMBED, 0.0, 0.02), g.normal(EMBED, 0.0, 0.02)
+    tokens = np.zeros(BATCH * TOKENS * EMBED, np.float32)
+    steps, elapsed = 0, 0.0
+    while steps == 0 or elapsed < seconds:
+        begin = time.perf_counter()
+        oracle.extract_patches(images, BATCH, CHANNELS, IMAGE, IMAGE, PATCH)
+        oracle.broadcast(tokens, cls, EMBED, TOKENS * EMBED, BATCH)
+        oracle.add_broadcast(tokens, pos, TOKENS * EMBED, BATCH)
+        oracle.layer_norm(x, gamma, beta, 1e-6)
+        oracle.softmax(logits)
+        elapsed += time.perf_counter() - begin
+        steps += 1
+    per_step = elapsed / steps
+    return {"value": round(STEP_BYTES / per_step / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": f"{steps} full batch-32 steps (gather, cls, pos add, LN [6304,192], "
+                      f"softmax [18912,197]) of the oracle, {elapsed:.1f} s, single thread, "
+                      f"{per_step * 1e3:.1f} ms/step; host has {os.cpu_count()} logical CPUs"}
+
+
+def counters(torch, cuvit, pools):
+    """For rocprofv3 --pmc passes: one plain copy of known size, then each
+    kernel over distinct cold sets. Prints what ran, in order."""
+    launch = pools.launchers(cuvit)
+    copy_bytes = 256 << 20
+    source = torch.randn(copy_bytes // 4, device="cuda")
+    target = torch.empty_like(source)
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    target.copy_(source)
+    torch.cuda.synchronize()
+    print(f"copy calibration: {copy_bytes} bytes read, {copy_bytes} bytes written", flush=True)
+    for name in ("layer_norm", "softmax", "extract_patches", "broadcast", "add_broadcast"):
+        for i in range(3):
+            flush.fill_(i)  # evict the Infinity Cache between launches
+            torch.cuda.synchronize()
+            launch[name](i)
+            torch.cuda.synchronize()
+        print(f"{name}: 3 cold launches, {BYTES[name]} algorithmic bytes each", flush=True)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path shards by image with no exchange; see the design notes)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import cuvit_amd as cuvit
+
+    cuvit.library()
+    device = torch.device("cuda:0")
+    pools = Pools(torch, device)
+    torch.cuda.synchronize()
+    if args.mode == "counters":
+        counters(torch, cuvit, pools)
+        return
+
+    launch = pools.launchers(cuvit)
+    for i in range(args.warmup):
+        step(launch, i)
+    torch.cuda.synchronize()
+
+    # K timed steps, one graph, rotating sets.
+    ms_graph = timed_graph(torch, lambda: [step(launch, i) for i in range(args.steps)], 1)
+    ms_per_step = ms_graph / args.steps
+
+    # Per-kernel launch durations: back-to-back launches over each pool (cold),
+    # and over one set (Infinity-Cache warm).
+    kernels = {}
+    for name, count in (("layer_norm", pools.ln_sets), ("softmax", pools.sm_sets),
+                        ("extract_patches", pools.px_sets), ("broadcast", pools.tok_sets),
+                        ("add_broadcast", pools.tok_sets)):
+        repeats = max(1, 400 // count)
+        cold_ms = timed_graph(torch, lambda: [launch[name](i) for i in range(count)], repeats) / count
+        warm_ms = timed_graph(torch, lambda: [launch[name](0) for _ in range(64)], 4) / 64
+        kernels[name] = {
+            "us_per_launch": round(cold_ms * 1e3, 3),
+            "GBps": round(BYTES[name] / (cold_ms * 1e-3) / 1e9, 1),
+            "frac_of_peak": round(BYTES[name] / (cold_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "warm_us_per_launch": round(warm_ms * 1e3, 3),
+            "warm_GBps": round(BYTES[name] / (warm_ms * 1e-3) / 1e9, 1),
+            "bytes": BYTES[name],
+            "launches_timed": count * repeats,
+        }
+    dominant = max(("layer_norm", "softmax", "extract_patches", "add_broadcast"),
+                   key=lambda n: kernels[n]["us_per_launch"])
+    achieved = kernels[dominant]["GBps"]
+    value = STEP_BYTES / (ms_per_step * 1e-3) / 1e9
+
+    line = {
+        "metric": "achieved HBM GB/s (% of 8 TB/s) for LN/softmax/patch-gather, ViT-Tiny b32",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded device RNG), cold HBM: per-kernel rotating pools > 512 MB",
+        "config": {"workload": "ViT-Tiny/16 batch 32: patch gather [32,3,224,224]->[6272,768] + "
+                               "class token + positional add into [32,197,192], LayerNorm "
+                               "[6304,192], in-place softmax [18912,197]",
+                   "bytes_per_step": STEP_BYTES, "steps_in_one_hip_graph": args.steps},
+        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None},
+        "kernels": kernels,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
