@@ -17,6 +17,9 @@ value        algorithmic bytes of one step / measured time of one step (GB/s);
 roofline     the kernel with the largest share of the step: algorithmic bytes of
              one launch / its average launch duration, from HIP events around
              a graph of back-to-back launches of that kernel over its pool.
+copy ceiling a device-to-device copy of the same bytes over the same kind of
+             cold pools, per kernel: what any kernel of that size can reach.
+vit_tiny_forward  the full batch-32 forward (114 launches) as one HIP graph.
 cpu_baseline the CPU oracle (a restatement of the reference's CPU loops) on a
              bounded sample of the same workload, one core.
 
@@ -56,6 +59,7 @@ BYTES = {
 }
 STEP_BYTES = sum(BYTES.values())
 HBM_PEAK_GBS = 8000.0
+VIT_TINY_FLOPS_PER_IMAGE = 2.507e9  # GEMM flops of one 224x224 ViT-Tiny/16 forward
 POOL_BYTES = 640 << 20  # per kernel: > 2x the 256 MB Infinity Cache
 
 
@@ -144,6 +148,47 @@ def timed_graph(torch, body, replays: int) -> float:
     stop.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / replays
+
+
+def copy_ceiling(torch, device, nbytes: int) -> float:
+    """ms per device-to-device copy moving the same bytes (half read, half
+    written) over cold rotating buffers: the attainable bound at this size."""
+    half = nbytes // 2 // 16 * 16
+    sets = min(256, max(2, -(-POOL_BYTES // max(nbytes, 1))))
+    src = [torch.empty(half, dtype=torch.uint8, device=device) for _ in range(sets)]
+    dst = [torch.empty(half, dtype=torch.uint8, device=device) for _ in range(sets)]
+    ms = timed_graph(torch, lambda: [dst[i].copy_(src[i]) for i in range(sets)],
+                     max(1, 200 // sets)) / sets
+    del src, dst
+    return ms
+
+
+def vit_forward(torch, cuvit, device, batch: int, replays: int):
+    """ms per ViT-Tiny/16 forward at @p batch (random N(0, 0.02) weights, LN
+    gamma N(1, 0.02), written as a .cvw file and loaded), one HIP graph."""
+    import tempfile
+
+    import numpy as np
+
+    config = cuvit.default_config()
+    rng = np.random.default_rng(404)
+    writer = cuvit.WeightWriter()
+    for name, shape in cuvit.expected_tensor_names(config):
+        mean = 1.0 if name.endswith(("norm1.weight", "norm2.weight")) or name == "norm.weight" else 0.0
+        writer.add(name, (mean + 0.02 * rng.standard_normal(shape)).astype(np.float32))
+    with tempfile.TemporaryDirectory() as folder:
+        path = os.path.join(folder, "vit_tiny.cvw")
+        writer.write(path)
+        writer.close()
+        weights = cuvit.WeightFile(path)
+        model = cuvit.VisionTransformer(config, weights, batch)
+    images = torch.rand(batch * CHANNELS * IMAGE * IMAGE, device=device) * 2 - 1
+    logits = torch.empty(batch * config.classes, device=device)
+    model.forward(images, logits, batch)
+    torch.cuda.synchronize()
+    ms = timed_graph(torch, lambda: model.forward(images, logits, batch), replays)
+    model.close()
+    return ms
 
 
 def cpu_baseline(seconds: float):
@@ -236,8 +281,11 @@ def main():
         repeats = max(1, 400 // count)
         cold_ms = timed_graph(torch, lambda: [launch[name](i) for i in range(count)], repeats) / count
         warm_ms = timed_graph(torch, lambda: [launch[name](0) for _ in range(64)], 4) / 64
+        copy_ms = copy_ceiling(torch, device, BYTES[name])
         kernels[name] = {
             "us_per_launch": round(cold_ms * 1e3, 3),
+            "copy_us_same_bytes": round(copy_ms * 1e3, 3),
+            "frac_of_copy": round(copy_ms / cold_ms, 3),
             "GBps": round(BYTES[name] / (cold_ms * 1e-3) / 1e9, 1),
             "frac_of_peak": round(BYTES[name] / (cold_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "warm_us_per_launch": round(warm_ms * 1e3, 3),
@@ -272,6 +320,12 @@ def main():
                      "traffic": None},
         "kernels": kernels,
     }
+    model_ms = vit_forward(torch, cuvit, device, BATCH, 20)
+    line["vit_tiny_forward"] = {
+        "batch": BATCH, "ms_per_forward": round(model_ms, 4),
+        "images_per_s": round(BATCH / (model_ms * 1e-3), 1),
+        "gemm_tflops": round(VIT_TINY_FLOPS_PER_IMAGE * BATCH / (model_ms * 1e-3) / 1e12, 2),
+        "launches": 114, "note": "fp32 end-to-end forward, one HIP graph; MFMA fp32 peak 157.3 TFLOP/s"}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)
