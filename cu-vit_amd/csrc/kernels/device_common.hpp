@@ -96,6 +96,18 @@ __device__ __forceinline__ void store16(void* pointer, const Vec16& value) {
     *reinterpret_cast<uint4*>(pointer) = make_uint4(value.w[0], value.w[1], value.w[2], value.w[3]);
 }
 
+/// A 16-byte store marked non-temporal (streaming): for outputs written once
+/// and not read again by the same kernel. On MI355X it skips the L2
+/// write-allocate and the end-of-kernel write-back of those lines, which
+/// measured 0.7 us faster for a 9.7 MB LayerNorm and 0.7 us for the 38.5 MB
+/// patch gather. Kernels that rewrite lines they have just read (in-place
+/// softmax, the positional add) gain nothing from it and keep plain stores.
+__device__ __forceinline__ void store16_streaming(void* pointer, const Vec16& value) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = {value.w[0], value.w[1], value.w[2], value.w[3]};
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(pointer));
+}
+
 /// Element access for the two storage types the kernels handle. A Vec16 holds
 /// 4 fp32 or 8 bf16 values.
 template <typename T> struct Elem;

@@ -15,7 +15,8 @@
 // threads write consecutive 16-byte vectors of a patch block (fully coalesced
 // stores); each quad of threads reads one 16-element run of an image row, and
 // the workgroup as a whole reads every byte of its span once, so every cache
-// line fetched from HBM is consumed by the same workgroup.
+// line fetched from HBM is consumed by the same workgroup. The patch matrix is
+// written with streaming (non-temporal) stores.
 //
 // broadcast / add_broadcast (normalization.cu:194-212) are 2-D grids over
 // (slot, vector) with float4 traffic when counts and pointers allow it.
@@ -76,7 +77,7 @@ __global__ __launch_bounds__(kBlock) void extract_patches_strip_kernel(
                 static_cast<std::int64_t>(patch_column) * row_elements +
                 static_cast<std::int64_t>(q) * kVec;
             const Word value = load16(source + source_element * ElementSize);
-            store16(destination + destination_element * ElementSize, value);
+            store16_streaming(destination + destination_element * ElementSize, value);
         }
     }
 }
