@@ -20,6 +20,7 @@ roofline     the kernel with the largest share of the step: algorithmic bytes of
 copy ceiling a device-to-device copy of the same bytes over the same kind of
              cold pools, per kernel: what any kernel of that size can reach.
 vit_tiny_forward  the full batch-32 forward (114 launches) as one HIP graph.
+vit_base_b64_bf16 the bf16 twins at ViT-Base/16 batch-64 shapes, cold.
 cpu_baseline the CPU oracle (a restatement of the reference's CPU loops) on a
              bounded sample of the same workload, one core.
 
@@ -191,6 +192,60 @@ def vit_forward(torch, cuvit, device, batch: int, replays: int):
     return ms
 
 
+def vit_base_bf16(torch, cuvit, device):
+    """ViT-Base/16 batch-64 shapes with bf16 activations: cold per-launch times
+    of LN [12608, 768], softmax [151296, 197] in place, the patch gather
+    [64, 3, 224, 224] and FC1 with the GELU epilogue (M 12608, N 3072, K 768)."""
+    rows, embed, hidden, heads, batch = 64 * TOKENS, 768, 3072, 12, 64
+    bf = torch.bfloat16
+    results = {}
+
+    def pool(count, nbytes_per_set):
+        sets = max(2, -(-POOL_BYTES // nbytes_per_set))
+        return [torch.randn(count, device=device).to(bf) for _ in range(sets)]
+
+    def record(name, nbytes, launch, sets):
+        ms = timed_graph(torch, lambda: [launch(i) for i in range(sets)], max(1, 200 // sets)) / sets
+        results[name] = {"us_per_launch": round(ms * 1e3, 3), "bytes": nbytes,
+                         "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                         "frac_of_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        return ms
+
+    ln_bytes = rows * embed * 4 + 2 * embed * 4
+    x = pool(rows * embed, ln_bytes)
+    y = [torch.empty_like(t) for t in x]
+    gamma = 1.0 + 0.02 * torch.randn(embed, device=device)
+    beta = 0.02 * torch.randn(embed, device=device)
+    record("layer_norm", ln_bytes,
+           lambda i: cuvit.layer_norm(x[i], gamma, beta, y[i], rows, embed, 1e-6), len(x))
+    del x, y
+    sm_rows = batch * heads * TOKENS
+    sm_bytes = sm_rows * TOKENS * 4
+    logits = pool(sm_rows * TOKENS, sm_bytes)
+    record("softmax", sm_bytes,
+           lambda i: cuvit.softmax(logits[i], logits[i], sm_rows, TOKENS), len(logits))
+    del logits
+    px_bytes = batch * CHANNELS * IMAGE * IMAGE * 4
+    images = pool(batch * CHANNELS * IMAGE * IMAGE, px_bytes)
+    patches = [torch.empty_like(t) for t in images]
+    record("extract_patches", px_bytes,
+           lambda i: cuvit.extract_patches(images[i], patches[i], batch, CHANNELS, IMAGE, IMAGE, PATCH),
+           len(images))
+    del images, patches
+    a = [torch.randn(rows * embed, device=device).to(bf) for _ in range(2)]
+    w = (0.02 * torch.randn(hidden * embed, device=device)).to(bf)
+    bias = 0.02 * torch.randn(hidden, device=device)
+    c = [torch.empty(rows * hidden, device=device, dtype=bf) for _ in range(2)]
+    problem = cuvit.gemm_problem(rows, hidden, embed, cuvit.TRANSPOSED)
+    problem.epilogue.gelu = 1
+    ms = record("fc1_gelu_gemm", 2 * (rows * embed + hidden * embed + rows * hidden),
+                lambda i: cuvit.gemm(a[i], w, bias, c[i], problem), 2)
+    flops = 2.0 * rows * hidden * embed
+    results["fc1_gelu_gemm"]["TFLOPs"] = round(flops / (ms * 1e-3) / 1e12, 2)
+    results["fc1_gelu_gemm"]["frac_of_bf16_mfma_peak"] = round(flops / (ms * 1e-3) / 2.5e15, 4)
+    return results
+
+
 def cpu_baseline(seconds: float):
     """The CPU oracle over the same workload, one core, until @p seconds of
     measured work (at least one full step)."""
@@ -326,6 +381,7 @@ def main():
         "images_per_s": round(BATCH / (model_ms * 1e-3), 1),
         "gemm_tflops": round(VIT_TINY_FLOPS_PER_IMAGE * BATCH / (model_ms * 1e-3) / 1e12, 2),
         "launches": 114, "note": "fp32 end-to-end forward, one HIP graph; MFMA fp32 peak 157.3 TFLOP/s"}
+    line["vit_base_b64_bf16"] = vit_base_bf16(torch, cuvit, device)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)

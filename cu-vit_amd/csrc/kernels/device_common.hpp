@@ -69,15 +69,10 @@ __device__ __forceinline__ float bf16_to_float(std::uint16_t bits) {
     return __uint_as_float(static_cast<std::uint32_t>(bits) << 16);
 }
 
-/// Rounds a float to bf16 bits, to nearest with ties to even. NaN stays NaN
-/// (a quiet bit is forced so the truncation cannot turn it into infinity).
+/// Rounds a float to bf16 bits, to nearest with ties to even, on gfx950's
+/// conversion unit (v_cvt_pk_bf16_f32); NaN stays a quiet NaN.
 __device__ __forceinline__ std::uint16_t float_to_bf16(float value) {
-    const std::uint32_t bits = __float_as_uint(value);
-    if ((bits & 0x7F800000U) == 0x7F800000U && (bits & 0x007FFFFFU) != 0) {
-        return static_cast<std::uint16_t>((bits >> 16) | 0x0040U);
-    }
-    const std::uint32_t rounding = 0x7FFFU + ((bits >> 16) & 1U);
-    return static_cast<std::uint16_t>((bits + rounding) >> 16);
+    return __builtin_bit_cast(std::uint16_t, static_cast<__bf16>(value));
 }
 
 // -- 16-byte vectors ----------------------------------------------------------

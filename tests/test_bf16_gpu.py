@@ -145,3 +145,18 @@ def test_gemm_bf16_vit_base_fc1_gelu(cuvit, oracle, device):
     pre = oracle.gemm_transposed(sample, w, bias, rows.size, n, k)
     scale = oracle.term_magnitudes(sample, w, rows.size, n, k, True)
     require_gemm_close(actual[rows], oracle.gelu(pre), scale, "ViT-Base FC1 + GELU (bf16)")
+
+
+def test_softmax_bf16_paths_agree_bitwise(cuvit, oracle, device):
+    """151296 rows take the staged path, a handful of rows the register path;
+    a row's bits must not depend on which (batch invariance)."""
+    rows, columns = 151296, 197
+    bits, _ = bf16_inputs(oracle, 909, rows * columns)
+    x = bf16_tensor(bits, device)
+    cuvit.softmax(x, x, rows, columns)
+    full = bf16_bits(x).reshape(rows, columns)
+    for start in (0, 7, 75000, rows - 5):
+        part = bf16_tensor(bits.reshape(rows, columns)[start:start + 5], device)
+        cuvit.softmax(part, part, 5, columns)
+        require_exact(bf16_bits(part).reshape(5, columns), full[start:start + 5],
+                      f"bf16 rows {start}.. differ between paths")

@@ -281,3 +281,22 @@ def test_invalid_arguments(cuvit, device):
         cuvit.gelu(None, buffer, 4)
     with pytest.raises(cuvit.InvalidArgument):
         cuvit.layer_norm(buffer, None, buffer, buffer, 2, 4)
+
+
+@pytest.mark.parametrize("columns", [197, 64, 1000])
+def test_softmax_staged_path_matches_oracle_and_register_path(cuvit, oracle, device, columns):
+    """Large row counts take the LDS-staged path; it must agree with the oracle
+    and give the same bits per row as the register path small launches take."""
+    rows = 40_003
+    x = oracle.generator(columns + 7).normal(rows * columns, 0.0, 4.0).reshape(rows, columns)
+    dx = to_device(x, device)
+    cuvit.softmax(dx, dx, rows, columns)
+    actual = to_host(dx)
+    sample = np.r_[0:16, rows // 2:rows // 2 + 16, rows - 16:rows]
+    expected = oracle.softmax(x[sample])
+    require_close(actual[sample], expected, "staged softmax", 1.0e-4, 1.0e-6)
+    require_max_abs(actual[sample], expected, MAX_ABS_FP32, "staged softmax max-abs")
+    for start in (0, 5, rows - 3):
+        part = to_device(x[start:start + 3], device)
+        cuvit.softmax(part, part, part.shape[0], columns)
+        require_exact(to_host(part), actual[start:start + 3], f"rows {start}.. differ between paths")
