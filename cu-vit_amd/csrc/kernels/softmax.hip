@@ -5,20 +5,31 @@
 // exp(x - max) / sum(exp(x - max)). input == output is allowed; the model runs
 // it in place over the attention logits (src/model/vit.cu:225).
 //
-// Register path (rows up to 64 * kMaxTerms columns). One wavefront owns a row
-// at a time: lane l holds columns l, l + 64, l + 128, ... as its terms, loaded
-// straight from HBM (consecutive lanes read consecutive elements, so each load
-// instruction is one contiguous 256-byte span for fp32). The row stays in
-// registers from the max through the exponentials to the scaled store, so HBM
-// sees exactly one read and one write per element. Rows of 197 floats are not
-// 16-byte aligned, and measured on MI355X this per-element layout beats both
-// staging 4-row blocks through LDS as aligned dwordx4 traffic and one block of
-// rows per single-wave workgroup, because it keeps more rows in flight per CU.
+// Each row is reduced by a team of L lanes: column c is lane c % L's
+// (c / L)-th term, the lane folds its terms in order, then a fixed DPP tree
+// combines the team. The team width depends only on the element type and the
+// row width: bf16 rows up to 256 wide use 16-lane teams (four rows per
+// wavefront, one quarter of the reduction instructions per row), everything
+// else a full 64-lane wavefront. Measured on MI355X, the 16-lane teams cut the
+// [151296, 197] bf16 softmax from 41.9 us to 27 us, while fp32 at ViT-Tiny
+// batch 32 stays fastest on full wavefronts. Both paths below give a row the
+// same bits for a given (type, width), wherever the row sits in a launch,
+// which is what keeps a batch bitwise equal to its images run one at a time.
 //
-// The reduction order is fixed by column index alone: column c is lane
-// c % 64's (c / 64)-th term, then the fixed wavefront tree combines the lanes.
-// A row therefore gives the same bits wherever it sits in a launch, which is
-// what keeps a batch bitwise equal to its images run one at a time.
+// Register path: each team loads its row's terms straight from HBM, keeps
+// them in registers from the max through the exponentials to the scaled
+// store, so HBM sees one read and one write per element. With full
+// wavefronts consecutive lanes read consecutive elements (one contiguous
+// 256-byte span per fp32 load instruction); rows of 197 floats are not
+// 16-byte aligned, and at ViT-Tiny batch 32 this beats staging through LDS
+// because it keeps more rows in flight per CU.
+//
+// Staged path: R rows of any width are `columns` 16-byte vectors (R = 4 fp32,
+// 8 bf16), so each wavefront moves an R-row block between HBM and a
+// wave-private LDS tile with aligned dwordx4 traffic, and prefetches its next
+// block into registers while it reduces the current one out of LDS. It runs
+// for every bf16 team-of-16 row when the pointers allow and for wider or fp32
+// rows from a row count that fills the chip several times over.
 //
 // Exponentials are exp2((x - max) * log2(e)) on the hardware exp2. x - max is
 // exact at x = max, where the largest outputs sit, and the relative error of an
@@ -26,15 +37,6 @@
 // unit's ~1 ulp), so it is largest where the output is smallest: under 1e-6
 // absolute for every output, far inside the reference test's 1e-4 relative
 // tolerance (tests/elementwise_test.cu:254-255).
-//
-// Staged path (the same rows at large row counts). R rows of any width are
-// `columns` 16-byte vectors (R = 4 fp32, 8 bf16), so each wavefront moves an
-// R-row block between HBM and a wave-private LDS tile with aligned dwordx4
-// traffic and reduces each row out of LDS in the same lane / term order and
-// with the same arithmetic as the register path, so both paths give the same
-// bits for a row. Which one runs depends only on the row count (measured:
-// the register path wins at ViT-Tiny batch 32, the staged path from ViT-Base
-// batch 64 up, 43 us vs 55 us for [151296, 197] bf16).
 //
 // Streaming path (rows wider than the register path holds): one wavefront per
 // row with an online max: a single streaming pass keeps a running (max, sum)
@@ -54,74 +56,125 @@ constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr float kLog2e = 1.4426950408889634F;
 
-/// Rows the register path holds: up to 64 * kMaxTerms columns.
+/// Terms per lane the register and staged paths hold.
 constexpr int kMaxTerms = 16;
+/// Widest row a 16-lane team takes.
+constexpr int kTeamColumns = 16 * kMaxTerms;
 
 /// exp(x - max).
 __device__ __forceinline__ float shifted_exp(float x, float max) {
     return __builtin_amdgcn_exp2f((x - max) * kLog2e);
 }
 
-template <typename T, int J>
+/// All-reduce over a team of L lanes (16: one DPP row; 64: the wavefront).
+template <int L, typename Op> __device__ __forceinline__ float team_allreduce(float value, Op op) {
+    static_assert(L == 16 || L == 64, "teams are 16 or 64 lanes");
+    if constexpr (L == 16) {
+        return row16_allreduce(value, op);
+    } else {
+        return wave_allreduce(value, op);
+    }
+}
+
+/// Softmax of one row whose J terms per lane are in @p x (-inf past the row):
+/// on return x holds the outputs. Team lane @p t holds columns t + L * j.
+template <int L, int J>
+__device__ __forceinline__ void softmax_terms(float (&x)[J], int t, int columns) {
+    float maximum = x[0];
+#pragma unroll
+    for (int j = 1; j < J; ++j) {
+        maximum = fmaxf(maximum, x[j]);
+    }
+    const float row_maximum = team_allreduce<L>(maximum, Max{});
+    float sum = 0.F;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        x[j] = t + L * j < columns ? shifted_exp(x[j], row_maximum) : 0.F;
+        sum += x[j];
+    }
+    const float inverse = 1.0F / team_allreduce<L>(sum, Sum{});
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        x[j] *= inverse;
+    }
+}
+
+template <typename T, int L, int J>
 __global__ __launch_bounds__(kBlock) void softmax_rows_kernel(const T* input, T* output, int rows,
                                                               int columns) {
+    constexpr int kTeams = kWave / L;
     const int lane = lane_id();
+    const int t = lane % L;
+    const std::int64_t groups = (static_cast<std::int64_t>(rows) + kTeams - 1) / kTeams;
     const std::int64_t waves = static_cast<std::int64_t>(gridDim.x) * kWavesPerBlock;
 
-    for (std::int64_t row = static_cast<std::int64_t>(blockIdx.x) * kWavesPerBlock +
-                            threadIdx.x / kWave;
-         row < rows; row += waves) {
+    for (std::int64_t group = static_cast<std::int64_t>(blockIdx.x) * kWavesPerBlock +
+                              threadIdx.x / kWave;
+         group < groups; group += waves) {
+        const std::int64_t row = group * kTeams + lane / L;
+        const bool here = row < rows;
         const T* const source = input + row * columns;
         T* const destination = output + row * columns;
 
         float x[J];
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            const int column = lane + kWave * j;
-            x[j] = column < columns ? Elem<T>::load(source + column) : -INFINITY;
+            const int column = t + L * j;
+            x[j] = here && column < columns ? Elem<T>::load(source + column) : -INFINITY;
         }
-
-        float maximum = x[0];
+        softmax_terms<L, J>(x, t, columns);
+        if (here) {
 #pragma unroll
-        for (int j = 1; j < J; ++j) {
-            maximum = fmaxf(maximum, x[j]);
-        }
-        const float row_maximum = wave_allreduce(maximum, Max{});
-
-        float sum = 0.F;
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const int column = lane + kWave * j;
-            x[j] = column < columns ? shifted_exp(x[j], row_maximum) : 0.F;
-            sum += x[j];
-        }
-        const float inverse = 1.0F / wave_allreduce(sum, Sum{});
-
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const int column = lane + kWave * j;
-            if (column < columns) {
-                Elem<T>::store(destination + column, x[j] * inverse);
+            for (int j = 0; j < J; ++j) {
+                const int column = t + L * j;
+                if (column < columns) {
+                    Elem<T>::store(destination + column, x[j]);
+                }
             }
         }
     }
 }
 
-template <typename T, int J>
+/// 16-byte vectors of an R-row block each lane prefetches: blocks up to
+/// 64 * kPrefetch vectors, which covers every row the staged path takes.
+constexpr int kPrefetch = 4;
+
+template <typename T, int L, int J>
 __global__ __launch_bounds__(kBlock) void softmax_staged_kernel(const T* input, T* output, int rows,
                                                                 int columns) {
     constexpr int R = Elem<T>::kPerVec;
+    constexpr int kTeams = kWave / L;
+    constexpr int kPasses = (R + kTeams - 1) / kTeams;
     extern __shared__ Vec16 lds[];
     const int lane = lane_id();
+    const int t = lane % L;
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     Vec16* const tile = lds + wave * columns;
     T* const tile_elements = reinterpret_cast<T*>(tile);
     const std::int64_t blocks = (static_cast<std::int64_t>(rows) + R - 1) / R;
+    const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * kWavesPerBlock;
+
+    // The next full block of this wavefront, held in registers while the
+    // current one is reduced.
+    Vec16 ahead[kPrefetch];
+    auto prefetch = [&](std::int64_t block) {
+        if (block < blocks && (block + 1) * R <= rows) {
+            const T* const source = input + block * R * columns;
+#pragma unroll
+            for (int i = 0; i < kPrefetch; ++i) {
+                const int v = lane + kWave * i;
+                if (v < columns) {
+                    ahead[i] = load16(source + static_cast<std::int64_t>(v) * R);
+                }
+            }
+        }
+    };
+    prefetch(static_cast<std::int64_t>(blockIdx.x) * kWavesPerBlock + wave);
 
     // Every wavefront of the workgroup runs the same iterations (a block past
     // the end is simply empty), so the barriers below are uniform.
     for (std::int64_t base = static_cast<std::int64_t>(blockIdx.x) * kWavesPerBlock; base < blocks;
-         base += static_cast<std::int64_t>(gridDim.x) * kWavesPerBlock) {
+         base += step) {
         const std::int64_t block = base + wave;
         const std::int64_t first_row = block * R;
         const int rows_here =
@@ -130,8 +183,12 @@ __global__ __launch_bounds__(kBlock) void softmax_staged_kernel(const T* input, 
         T* const destination = output + first_row * columns;
 
         if (rows_here == R) {
-            for (int v = lane; v < columns; v += kWave) {
-                tile[v] = load16(source + static_cast<std::int64_t>(v) * R);
+#pragma unroll
+            for (int i = 0; i < kPrefetch; ++i) {
+                const int v = lane + kWave * i;
+                if (v < columns) {
+                    tile[v] = ahead[i];
+                }
             }
         } else {
             for (int i = lane; i < rows_here * columns; i += kWave) {
@@ -139,46 +196,28 @@ __global__ __launch_bounds__(kBlock) void softmax_staged_kernel(const T* input, 
             }
         }
         __syncthreads();
+        prefetch(block + step);
 
-        float x[R][J];
+        // Each lane writes back exactly the elements it read, so the
+        // reductions need no barrier between them.
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
+        for (int pass = 0; pass < kPasses; ++pass) {
+            const int r = pass * kTeams + lane / L;
+            const bool here = r < rows_here;
+            float x[J];
 #pragma unroll
             for (int j = 0; j < J; ++j) {
-                const int column = lane + kWave * j;
-                x[r][j] = (r < rows_here && column < columns)
-                              ? Elem<T>::load(tile_elements + r * columns + column)
-                              : -INFINITY;
+                const int column = t + L * j;
+                x[j] = here && column < columns ? Elem<T>::load(tile_elements + r * columns + column)
+                                                : -INFINITY;
             }
-        }
-        float inverse[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float maximum = x[r][0];
-#pragma unroll
-            for (int j = 1; j < J; ++j) {
-                maximum = fmaxf(maximum, x[r][j]);
-            }
-            const float row_maximum = wave_allreduce(maximum, Max{});
-            float sum = 0.F;
-#pragma unroll
-            for (int j = 0; j < J; ++j) {
-                const int column = lane + kWave * j;
-                x[r][j] = column < columns ? shifted_exp(x[r][j], row_maximum) : 0.F;
-                sum += x[r][j];
-            }
-            inverse[r] = 1.0F / wave_allreduce(sum, Sum{});
-        }
-        __syncthreads();
-
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if (r < rows_here) {
+            softmax_terms<L, J>(x, t, columns);
+            if (here) {
 #pragma unroll
                 for (int j = 0; j < J; ++j) {
-                    const int column = lane + kWave * j;
+                    const int column = t + L * j;
                     if (column < columns) {
-                        Elem<T>::store(tile_elements + r * columns + column, x[r][j] * inverse[r]);
+                        Elem<T>::store(tile_elements + r * columns + column, x[j]);
                     }
                 }
             }
@@ -232,46 +271,65 @@ __global__ __launch_bounds__(kBlock) void softmax_online_kernel(const T* input, 
 }
 
 /// Workgroups per compute unit before the grid loops: 32 waves, the most a CU
-/// holds at this kernel's register use, measured fastest at ViT shapes.
+/// holds at the register path's register use, measured fastest at ViT shapes.
 constexpr int kBlocksPerCu = 8;
+/// The staged path keeps a prefetched block in registers: 16 waves per CU
+/// measured fastest ([151296, 197] bf16: 27.0 us against 29.8 us at 32).
+constexpr int kStagedBlocksPerCu = 4;
 
-/// Row counts from which the staged path is used: more than four rows per
-/// wavefront once every compute unit is full.
+/// Row counts from which full-wavefront rows take the staged path: more than
+/// four rows per wavefront once every compute unit is full.
 std::int64_t staged_threshold() { return static_cast<std::int64_t>(compute_units()) * 128; }
 
-template <typename T, int J>
+template <typename T, int L, int J>
 hipError_t launch_rows(const T* input, T* output, int rows, int columns, hipStream_t stream) {
     constexpr int R = Elem<T>::kPerVec;
-    if (rows >= staged_threshold() && aligned16(input) && aligned16(output)) {
+    const bool staged = L < kWave || rows >= staged_threshold();
+    if (staged && columns <= kWave * kPrefetch && aligned16(input) && aligned16(output)) {
         const std::int64_t blocks = (static_cast<std::int64_t>(rows) + R - 1) / R;
-        const unsigned int grid = stride_grid(blocks, kWavesPerBlock, kBlocksPerCu);
+        const unsigned int grid = stride_grid(blocks, kWavesPerBlock, kStagedBlocksPerCu);
         const std::size_t lds = static_cast<std::size_t>(kWavesPerBlock) * columns * sizeof(Vec16);
-        softmax_staged_kernel<T, J><<<grid, kBlock, lds, stream>>>(input, output, rows, columns);
+        softmax_staged_kernel<T, L, J><<<grid, kBlock, lds, stream>>>(input, output, rows, columns);
         return hipGetLastError();
     }
-    const unsigned int grid = stride_grid(rows, kWavesPerBlock, kBlocksPerCu);
-    softmax_rows_kernel<T, J><<<grid, kBlock, 0, stream>>>(input, output, rows, columns);
+    const std::int64_t teams = kWave / L;
+    const unsigned int grid = stride_grid((rows + teams - 1) / teams, kWavesPerBlock, kBlocksPerCu);
+    softmax_rows_kernel<T, L, J><<<grid, kBlock, 0, stream>>>(input, output, rows, columns);
     return hipGetLastError();
+}
+
+/// Picks J, the terms per lane, for a team of L lanes. Rounding J up adds
+/// terms that are -inf before and 0 after the exponential, which changes no
+/// bit of the max or the sum, so the choice never changes a result.
+template <typename T, int L>
+hipError_t launch_team(const T* input, T* output, int rows, int columns, hipStream_t stream) {
+    switch ((columns + L - 1) / L) {
+    case 1: return launch_rows<T, L, 1>(input, output, rows, columns, stream);
+    case 2: return launch_rows<T, L, 2>(input, output, rows, columns, stream);
+    case 3: return launch_rows<T, L, 3>(input, output, rows, columns, stream);
+    case 4: return launch_rows<T, L, 4>(input, output, rows, columns, stream);
+    case 5:
+    case 6: return launch_rows<T, L, 6>(input, output, rows, columns, stream);
+    case 7:
+    case 8: return launch_rows<T, L, 8>(input, output, rows, columns, stream);
+    case 9:
+    case 10: return launch_rows<T, L, 10>(input, output, rows, columns, stream);
+    case 11:
+    case 12:
+    case 13: return launch_rows<T, L, 13>(input, output, rows, columns, stream);
+    default: return launch_rows<T, L, 16>(input, output, rows, columns, stream);
+    }
 }
 
 template <typename T>
 hipError_t dispatch(const T* input, T* output, int rows, int columns, hipStream_t stream) {
-    if (columns <= kWave * kMaxTerms) {
-        switch ((columns + kWave - 1) / kWave) {
-        case 1: return launch_rows<T, 1>(input, output, rows, columns, stream);
-        case 2: return launch_rows<T, 2>(input, output, rows, columns, stream);
-        case 3: return launch_rows<T, 3>(input, output, rows, columns, stream);
-        case 4: return launch_rows<T, 4>(input, output, rows, columns, stream);
-        case 5:
-        case 6: return launch_rows<T, 6>(input, output, rows, columns, stream);
-        case 7:
-        case 8: return launch_rows<T, 8>(input, output, rows, columns, stream);
-        case 9:
-        case 10:
-        case 11:
-        case 12: return launch_rows<T, 12>(input, output, rows, columns, stream);
-        default: return launch_rows<T, 16>(input, output, rows, columns, stream);
+    if constexpr (sizeof(T) == 2) {
+        if (columns <= kTeamColumns) {
+            return launch_team<T, 16>(input, output, rows, columns, stream);
         }
+    }
+    if (columns <= kWave * kMaxTerms) {
+        return launch_team<T, kWave>(input, output, rows, columns, stream);
     }
     const unsigned int grid = stride_grid(rows, kWavesPerBlock, kBlocksPerCu);
     softmax_online_kernel<T><<<grid, kBlock, 0, stream>>>(input, output, rows, columns);
