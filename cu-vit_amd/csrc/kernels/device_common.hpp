@@ -115,6 +115,14 @@ template <> struct Elem<float> {
     __device__ __forceinline__ static void set(Vec16& v, int i, float x) { v.w[i] = __float_as_uint(x); }
     __device__ __forceinline__ static float load(const float* p) { return *p; }
     __device__ __forceinline__ static void store(float* p, float x) { *p = x; }
+    /// Copies element @p p into slot @p i of @p v without conversion.
+    __device__ __forceinline__ static void put_bits(Vec16& v, int i, const float* p) {
+        v.w[i] = __float_as_uint(*p);
+    }
+    /// Writes slot @p i of @p v to @p p without conversion.
+    __device__ __forceinline__ static void store_bits(float* p, const Vec16& v, int i) {
+        *p = __uint_as_float(v.w[i]);
+    }
 };
 
 template <> struct Elem<std::uint16_t> {
@@ -130,6 +138,15 @@ template <> struct Elem<std::uint16_t> {
     }
     __device__ __forceinline__ static float load(const std::uint16_t* p) { return bf16_to_float(*p); }
     __device__ __forceinline__ static void store(std::uint16_t* p, float x) { *p = float_to_bf16(x); }
+    __device__ __forceinline__ static void put_bits(Vec16& v, int i, const std::uint16_t* p) {
+        const std::uint32_t bits = *p;
+        std::uint32_t& word = v.w[i >> 1];
+        word = (i & 1) ? ((word & 0x0000FFFFU) | (bits << 16)) : ((word & 0xFFFF0000U) | bits);
+    }
+    __device__ __forceinline__ static void store_bits(std::uint16_t* p, const Vec16& v, int i) {
+        const std::uint32_t word = v.w[i >> 1];
+        *p = static_cast<std::uint16_t>((i & 1) ? (word >> 16) : (word & 0xFFFFU));
+    }
 };
 
 /// True when @p pointer is 16-byte aligned.
