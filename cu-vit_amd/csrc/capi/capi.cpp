@@ -345,6 +345,36 @@ int cuvit_add_broadcast_f32(float* accumulator, const float* addend, int64_t cou
                     "add_broadcast launch");
 }
 
+int cuvit_attention_supported(int tokens, int head_dim) {
+    return detail::attention_supported(tokens, head_dim) ? 1 : 0;
+}
+
+int cuvit_attention_f32(const float* qkv, float* context, int images, int heads, int tokens,
+                        int head_dim, cuvit_stream_t stream) {
+    if (images == 0 || heads == 0 || tokens == 0 || head_dim == 0) {
+        return capi::ok();
+    }
+    if (images < 0 || heads < 0 || tokens < 0 || head_dim < 0) {
+        return capi::fail(CUVIT_ERROR_INVALID_ARGUMENT, "Attention extents cannot be negative");
+    }
+    if (qkv == nullptr || context == nullptr) {
+        return capi::fail(CUVIT_ERROR_INVALID_ARGUMENT, "Attention operands cannot be null");
+    }
+    if (!detail::attention_supported(tokens, head_dim)) {
+        return capi::fail(CUVIT_ERROR_INVALID_ARGUMENT,
+                          "Fused attention supports head_dim 64 and at most 256 tokens");
+    }
+    if (((reinterpret_cast<std::uintptr_t>(qkv) | reinterpret_cast<std::uintptr_t>(context)) & 15U) != 0) {
+        return capi::fail(CUVIT_ERROR_INVALID_ARGUMENT, "Fused attention needs 16-byte aligned operands");
+    }
+    if (capi::saturating_product(images, heads) > 65535) {
+        return capi::fail(CUVIT_ERROR_LENGTH, "Fused attention takes at most 65535 (image, head) pairs");
+    }
+    return from_hip(detail::attention_f32(qkv, context, images, heads, tokens, head_dim,
+                                          capi::as_hip(stream)),
+                    "attention launch");
+}
+
 int cuvit_broadcast_f32(float* destination, const float* source, int64_t count,
                         int64_t destination_stride, int batch, cuvit_stream_t stream) {
     if (count == 0 || batch == 0) {

@@ -1,16 +1,19 @@
 // VisionTransformer: the launch sequence of the reference's forward pass
 // (src/model/vit.cu:173-317) over arena-carved activations.
 //
-// Per block (run_block, vit.cu:173-261): LN1 -> QKV GEMM -> Q.K^T GEMM (alpha
-// 1/sqrt(head_dim), split batch over (image, head)) -> softmax in place ->
-// attention.V GEMM written straight into [tokens, heads * head_dim] -> proj
+// Per block (run_block, vit.cu:173-261): LN1 -> QKV GEMM -> attention -> proj
 // GEMM accumulating into the residual stream -> LN2 -> FC1 GEMM with the GELU
-// epilogue -> FC2 GEMM accumulating into the residual stream.
+// epilogue -> FC2 GEMM accumulating into the residual stream. Attention is
+// the reference's Q.K^T GEMM (alpha 1/sqrt(head_dim), split batch over
+// (image, head)) -> softmax in place -> attention.V GEMM written straight into
+// [tokens, heads * head_dim]; where the shape allows it runs as one fused
+// launch with bitwise the same result and no logits buffer.
 // Around the blocks (forward, vit.cu:263-317): patch gather -> embedding GEMM
 // into rows 1.. of each image -> class token into row 0 -> positional add ->
 // blocks -> final LN -> head GEMM on the class rows only.
 #include "cuvit/vit.hpp"
 
+#include "cuvit/capi.h"
 #include "cuvit/hip_check.hpp"
 #include "cuvit/kernels.hpp"
 
@@ -140,6 +143,10 @@ VisionTransformer::VisionTransformer(const VitConfig& config, const WeightFile& 
     head_weight_ = upload(weights_, file, "head.weight", {classes, embed});
     head_bias_ = upload(weights_, file, "head.bias", {classes});
 
+    // Attention runs fused (no logits buffer) whenever the shape allows.
+    fused_attention_ = cuvit_attention_supported(config_.token_count(), config_.head_dim()) != 0 &&
+                       static_cast<std::int64_t>(max_batch_) * config_.heads <= 65535;
+
     // Activation scratch for max_batch images, shared by every block.
     const Extent images = max_batch_;
     const Extent activation_counts[] = {
@@ -147,7 +154,7 @@ VisionTransformer::VisionTransformer(const VitConfig& config, const WeightFile& 
         images * tokens * embed,                  // residual stream
         images * tokens * embed,                  // normalized
         images * tokens * 3 * embed,              // packed q, k, v
-        images * config_.heads * tokens * tokens, // attention logits / weights
+        fused_attention_ ? 0 : images * config_.heads * tokens * tokens, // attention logits
         images * tokens * embed,                  // attention context
         images * tokens * hidden,                 // MLP hidden
     };
@@ -162,25 +169,15 @@ VisionTransformer::VisionTransformer(const VitConfig& config, const WeightFile& 
     }
 }
 
-void VisionTransformer::run_block(const BlockWeights& block, float* tokens, int batch,
-                                  hipStream_t stream) {
+void VisionTransformer::attention_unfused(int batch, hipStream_t stream) {
     const int token_count = config_.token_count();
     const int embed = config_.embed_dim;
     const int heads = config_.heads;
     const int head_dim = config_.head_dim();
-    const int hidden = config_.mlp_hidden;
-    const int rows = batch * token_count;
     const std::int64_t tokens_per_image = static_cast<std::int64_t>(token_count) * embed;
     const std::int64_t qkv_per_image = tokens_per_image * 3;
     const std::int64_t logits_per_head = static_cast<std::int64_t>(token_count) * token_count;
     const int qkv_row = 3 * embed;
-
-    launch_layer_norm(tokens, block.norm1_gamma, block.norm1_beta, normalized_, rows, embed,
-                      config_.layer_norm_epsilon, stream);
-
-    // [tokens, 3, heads, head_dim] in one projection.
-    launch_gemm(normalized_, block.qkv_weight, block.qkv_bias, qkv_,
-                gemm_problem(rows, qkv_row, embed, GemmLayout::kTransposed), stream);
 
     // Q.K^T per (image, head), read in place from the packed projection.
     GemmProblem logits = gemm_problem(token_count, token_count, head_dim, GemmLayout::kTransposed);
@@ -214,6 +211,33 @@ void VisionTransformer::run_block(const BlockWeights& block, float* tokens, int 
     context.batch.outer_stride_b = qkv_per_image;
     context.batch.outer_stride_c = tokens_per_image;
     launch_gemm(attention_, qkv_ + 2 * embed, nullptr, context_, context, stream);
+}
+
+void VisionTransformer::run_block(const BlockWeights& block, float* tokens, int batch,
+                                  hipStream_t stream) {
+    const int token_count = config_.token_count();
+    const int embed = config_.embed_dim;
+    const int heads = config_.heads;
+    const int head_dim = config_.head_dim();
+    const int hidden = config_.mlp_hidden;
+    const int rows = batch * token_count;
+    const int qkv_row = 3 * embed;
+
+    launch_layer_norm(tokens, block.norm1_gamma, block.norm1_beta, normalized_, rows, embed,
+                      config_.layer_norm_epsilon, stream);
+
+    // [tokens, 3, heads, head_dim] in one projection.
+    launch_gemm(normalized_, block.qkv_weight, block.qkv_bias, qkv_,
+                gemm_problem(rows, qkv_row, embed, GemmLayout::kTransposed), stream);
+
+    // softmax(Q.K^T / sqrt(head_dim)).V per (image, head) in one fused launch
+    // when the shape allows; it is bitwise equal to the three launches below.
+    if (fused_attention_) {
+        throw_on_error(cuvit_attention_f32(qkv_, context_, batch, heads, token_count, head_dim,
+                                           reinterpret_cast<cuvit_stream_t>(stream)));
+    } else {
+        attention_unfused(batch, stream);
+    }
 
     GemmProblem projection = gemm_problem(rows, embed, embed, GemmLayout::kTransposed);
     projection.epilogue.accumulate = true;

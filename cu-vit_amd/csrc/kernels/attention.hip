@@ -1,0 +1,277 @@
+// Fused attention for the ViT block: context = softmax(Q.K^T * scale).V per
+// (image, head), from the packed QKV projection, without materializing the
+// [images, heads, tokens, tokens] logits.
+//
+// The reference runs this as three launches (src/model/vit.cu:205-245): the
+// Q.K^T GEMM with alpha = 1/sqrt(head_dim) into the logits, softmax in place,
+// and the weights.V GEMM into the context. This kernel computes the very same
+// floating-point operations in the same order, so its output is bitwise equal
+// to those three launches of this library:
+//   * logits: the GEMM's v_mfma_f32_16x16x4_f32 over head_dim in k-blocks of
+//     16 (MFMA s of a block sums k = kb + s, kb + 4 + s, kb + 8 + s,
+//     kb + 12 + s), then alpha * sum, exactly as in the GEMM epilogue;
+//   * softmax: the max is exact in any order; the exponentials are the same
+//     exp2((x - max) * log2 e); the sum reproduces the full-wavefront softmax
+//     (one 64-lane team per row): lane c' of that team sums the columns
+//     c' + 64 j in order from +0, then the DPP tree (quad swap 1, quad swap 2,
+//     half-row mirror, row mirror) and (r0 + r1) + (r2 + r3) over the four
+//     row totals. Here the same 64 partial sums sit in the registers of the
+//     four lanes that hold a query row, and the tree is replayed with two
+//     cross-lane exchanges; probabilities are e * (1 / sum) as there;
+//   * weights.V: the GEMM's MFMA over keys in k-blocks of 16, keys past the
+//     token count contributing exact zeros.
+// The probabilities never leave registers: a lane of the logits tile holds
+// row l % 16 and keys 4 (l / 16) .. + 3 of each 16-key tile, which is
+// exactly the A fragment the weights.V MFMA consumes.
+//
+// Layout: qkv is [images, tokens, 3, heads, head_dim] and context is
+// [images, tokens, heads, head_dim] (src/model/vit.cu:199-245). A workgroup
+// owns one (image, head) and up to kWaves query tiles of 16 rows; K and V of
+// that (image, head) sit in LDS as [key][head_dim + 4] fp32 (padded rows give
+// conflict-free 16-byte fragment reads).
+#include "device_common.hpp"
+#include "launch.hpp"
+
+#include <cmath>
+
+namespace cuvit::detail {
+namespace {
+
+using namespace cuvit::device;
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kHeadDim = 64;          // head_dim this kernel handles
+constexpr int kPitch = kHeadDim + 4;  // floats per LDS row
+constexpr int kMaxKeyTiles = 16;      // up to 256 tokens
+constexpr float kLog2e = 1.4426950408889634F;
+
+__device__ __forceinline__ float shuffle_xor(float value, int mask) {
+    return __shfl_xor(value, mask, kWave);
+}
+
+template <int Waves>
+__global__ __launch_bounds__(Waves * kWave) void attention_kernel(const float* __restrict__ qkv,
+                                                                  float* __restrict__ context,
+                                                                  int heads, int tokens, float scale) {
+    extern __shared__ Vec16 lds_vectors[];
+    float* const keys = reinterpret_cast<float*>(lds_vectors);
+    const int key_tiles = (tokens + 15) / 16;
+    float* const values = keys + key_tiles * 16 * kPitch;
+
+    const int t = threadIdx.x;
+    const int lane = lane_id();
+    const int wave = t / kWave;
+    const int row_in_tile = lane & 15;
+    const int group = lane >> 4;
+
+    const int pair = blockIdx.y;
+    const int image = pair / heads;
+    const int head = pair - image * heads;
+    const int embed = heads * kHeadDim;
+    const std::int64_t qkv_row = 3 * static_cast<std::int64_t>(embed);
+    const float* const q_base = qkv + static_cast<std::int64_t>(image) * tokens * qkv_row + head * kHeadDim;
+    const float* const k_base = q_base + embed;
+    const float* const v_base = q_base + 2 * embed;
+
+    // K and V of this (image, head) into LDS; rows past the tokens are zero.
+    constexpr int kQuadsPerRow = kHeadDim / 4;
+    for (int q = t; q < key_tiles * 16 * kQuadsPerRow; q += Waves * kWave) {
+        const int row = q / kQuadsPerRow;
+        const int quad = q - row * kQuadsPerRow;
+        float4 k4 = make_float4(0.F, 0.F, 0.F, 0.F);
+        float4 v4 = k4;
+        if (row < tokens) {
+            k4 = *reinterpret_cast<const float4*>(k_base + row * qkv_row + 4 * quad);
+            v4 = *reinterpret_cast<const float4*>(v_base + row * qkv_row + 4 * quad);
+        }
+        *reinterpret_cast<float4*>(keys + row * kPitch + 4 * quad) = k4;
+        *reinterpret_cast<float4*>(values + row * kPitch + 4 * quad) = v4;
+    }
+    __syncthreads();
+
+    const int query_tile = blockIdx.x * Waves + wave;
+    const int q0 = query_tile * 16;
+    if (q0 >= tokens) {
+        return; // no barrier follows
+    }
+
+    // Q fragments: row q0 + l % 16 (clamped), head_dim chunk 4 (l / 16) of
+    // each k-block.
+    const int q_row = q0 + row_in_tile < tokens ? q0 + row_in_tile : tokens - 1;
+    Vec16 qf[kHeadDim / 16];
+#pragma unroll
+    for (int kb = 0; kb < kHeadDim / 16; ++kb) {
+        qf[kb] = load16(q_base + q_row * qkv_row + 16 * kb + 4 * group);
+    }
+
+    // Logits: lane holds row q0 + l % 16, keys 16 jt + 4 (l / 16) + r.
+    floatx4 s[kMaxKeyTiles];
+#pragma unroll
+    for (int jt = 0; jt < kMaxKeyTiles; ++jt) {
+        s[jt] = floatx4{0.F, 0.F, 0.F, 0.F};
+        if (jt < key_tiles) {
+#pragma unroll
+            for (int kb = 0; kb < kHeadDim / 16; ++kb) {
+                const Vec16 kf = load16(keys + (16 * jt + row_in_tile) * kPitch + 16 * kb + 4 * group);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    s[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(kf.w[e]),
+                                                                 __uint_as_float(qf[kb].w[e]), s[jt],
+                                                                 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    // Row max over the valid keys (exact in any order).
+    float maximum = -INFINITY;
+#pragma unroll
+    for (int jt = 0; jt < kMaxKeyTiles; ++jt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int key = 16 * jt + 4 * group + r;
+            s[jt][r] = scale * s[jt][r];
+            if (key < tokens) {
+                maximum = fmaxf(maximum, s[jt][r]);
+            }
+        }
+    }
+    maximum = fmaxf(maximum, shuffle_xor(maximum, 16));
+    maximum = fmaxf(maximum, shuffle_xor(maximum, 32));
+
+    // Exponentials; keys past the tokens become exact zeros.
+#pragma unroll
+    for (int jt = 0; jt < kMaxKeyTiles; ++jt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int key = 16 * jt + 4 * group + r;
+            s[jt][r] = key < tokens ? __builtin_amdgcn_exp2f((s[jt][r] - maximum) * kLog2e) : 0.F;
+        }
+    }
+
+    // The full-wavefront softmax's sum. Its lane c' = 16 a + 4 g + r sums
+    // columns c' + 64 j, j = 0..3: key tiles 4 j + a, element r of group g,
+    // all in this lane's registers.
+    float v[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float partial = 0.F;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                partial += s[4 * j + a][r];
+            }
+            v[a][r] = partial;
+        }
+    }
+    // Quad swaps: lane c' ^ 1, then c' ^ 2 (r ^ 1, r ^ 2 within this lane).
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        float w[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) w[r] = v[a][r] + v[a][r ^ 1];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[a][r] = w[r] + w[r ^ 2];
+    }
+    // Half-row mirror: c' & 7 -> 7 - (c' & 7), i.e. group g ^ 1, element 3 - r.
+    {
+        float partner[4][4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) partner[a][r] = shuffle_xor(v[a][r], 16);
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[a][r] = v[a][r] + partner[a][3 - r];
+    }
+    // Row mirror: c' & 15 -> 15 - (c' & 15), i.e. group g ^ 3, element 3 - r.
+    {
+        float partner[4][4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) partner[a][r] = shuffle_xor(v[a][r], 48);
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[a][r] = v[a][r] + partner[a][3 - r];
+    }
+    // Every lane of a 16-lane row now holds that row's total; the four rows
+    // combine as (r0 + r1) + (r2 + r3).
+    const float inverse = 1.0F / ((v[0][0] + v[1][0]) + (v[2][0] + v[3][0]));
+#pragma unroll
+    for (int jt = 0; jt < kMaxKeyTiles; ++jt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            s[jt][r] *= inverse;
+        }
+    }
+
+    // weights.V: lane provides weights[row][keys 16 jt + 4 g + e] (its own
+    // registers) and V[keys 16 jt + 4 g + e][16 dt + l % 16].
+    floatx4 out[kHeadDim / 16];
+#pragma unroll
+    for (int dt = 0; dt < kHeadDim / 16; ++dt) {
+        out[dt] = floatx4{0.F, 0.F, 0.F, 0.F};
+    }
+#pragma unroll
+    for (int jt = 0; jt < kMaxKeyTiles; ++jt) {
+        if (jt < key_tiles) {
+            const float* const v_rows = values + (16 * jt + 4 * group) * kPitch + row_in_tile;
+#pragma unroll
+            for (int dt = 0; dt < kHeadDim / 16; ++dt) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    out[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(v_rows[e * kPitch + 16 * dt], s[jt][e],
+                                                                   out[dt], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    // Lane holds context[row][16 dt + 4 (l / 16) .. + 3].
+    const int row = q0 + row_in_tile;
+    if (row < tokens) {
+        float* const destination = context +
+                                   (static_cast<std::int64_t>(image) * tokens + row) * embed +
+                                   head * kHeadDim + 4 * group;
+#pragma unroll
+        for (int dt = 0; dt < kHeadDim / 16; ++dt) {
+            *reinterpret_cast<floatx4*>(destination + 16 * dt) = out[dt];
+        }
+    }
+}
+
+constexpr int kWaves = 8;
+
+} // namespace
+
+bool attention_supported(int tokens, int head_dim) {
+    return head_dim == kHeadDim && tokens > 0 && tokens <= 16 * kMaxKeyTiles;
+}
+
+hipError_t attention_f32(const float* qkv, float* context, int images, int heads, int tokens,
+                         int head_dim, hipStream_t stream) {
+    if (!attention_supported(tokens, head_dim)) {
+        return hipErrorInvalidValue;
+    }
+    const int key_tiles = (tokens + 15) / 16;
+    const std::size_t lds = 2 * static_cast<std::size_t>(key_tiles) * 16 * kPitch * sizeof(float);
+    static const hipError_t opted = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(attention_kernel<kWaves>),
+        hipFuncAttributeMaxDynamicSharedMemorySize,
+        static_cast<int>(2 * 16 * kMaxKeyTiles * kPitch * sizeof(float)));
+    if (opted != hipSuccess) {
+        return opted;
+    }
+    const dim3 grid(static_cast<unsigned int>((key_tiles + kWaves - 1) / kWaves),
+                    static_cast<unsigned int>(images * heads));
+    const float scale = 1.0F / std::sqrt(static_cast<float>(head_dim));
+    attention_kernel<kWaves><<<grid, kWaves * kWave, lds, stream>>>(qkv, context, heads, tokens, scale);
+    return hipGetLastError();
+}
+
+} // namespace cuvit::detail

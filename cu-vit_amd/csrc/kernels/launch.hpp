@@ -66,6 +66,13 @@ hipError_t gemm_f32(const float* a, const float* b, const float* bias, float* c,
 hipError_t gemm_bf16(const std::uint16_t* a, const std::uint16_t* b, const float* bias,
                      std::uint16_t* c, const GemmArgs& args, hipStream_t stream);
 
+/// Fused softmax(Q.K^T / sqrt(head_dim)).V per (image, head) from the packed
+/// [images, tokens, 3, heads, head_dim] projection into [images, tokens,
+/// heads, head_dim]; bitwise equal to the GEMM -> softmax -> GEMM sequence.
+bool attention_supported(int tokens, int head_dim);
+hipError_t attention_f32(const float* qkv, float* context, int images, int heads, int tokens,
+                         int head_dim, hipStream_t stream);
+
 // Device facts used to shape grids, cached per device.
 int compute_units();
 

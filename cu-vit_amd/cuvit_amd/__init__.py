@@ -155,6 +155,8 @@ _SIGNATURES = {
     "cuvit_add_f32": (_I, [_P, _P, _L, _P]),
     "cuvit_add_broadcast_f32": (_I, [_P, _P, _L, _I, _P]),
     "cuvit_broadcast_f32": (_I, [_P, _P, _L, _L, _I, _P]),
+    "cuvit_attention_supported": (_I, [_I, _I]),
+    "cuvit_attention_f32": (_I, [_P, _P, _I, _I, _I, _I, _P]),
     "cuvit_weight_writer_create": (_I, [ctypes.POINTER(_P)]),
     "cuvit_weight_writer_add": (_I, [_P, ctypes.c_char_p, _I, ctypes.POINTER(_L), _P]),
     "cuvit_weight_writer_write": (_I, [_P, ctypes.c_char_p]),
@@ -295,6 +297,21 @@ def broadcast(destination, source, count: int, destination_stride: int, batch: i
               stream=None) -> None:
     check(library().cuvit_broadcast_f32(_ptr(destination), _ptr(source), count,
                                         destination_stride, batch, stream_handle(stream)))
+
+
+def attention_supported(tokens: int, head_dim: int) -> bool:
+    """True when the fused attention kernel covers (tokens, head_dim)."""
+    return bool(library().cuvit_attention_supported(tokens, head_dim))
+
+
+def attention(qkv, context, images: int, heads: int, tokens: int, head_dim: int,
+              stream=None) -> None:
+    """Fused softmax(Q.K^T / sqrt(head_dim)).V from the packed
+    [images, tokens, 3, heads, head_dim] projection into
+    [images, tokens, heads, head_dim]; an extension replacing the reference's
+    three attention launches (vit.cu:205-245) with bitwise the same result."""
+    check(library().cuvit_attention_f32(_ptr(qkv), _ptr(context), images, heads, tokens, head_dim,
+                                        stream_handle(stream)))
 
 
 class WeightWriter:

@@ -130,6 +130,19 @@ int cuvit_add_broadcast_f32(float* accumulator, const float* addend, int64_t cou
 int cuvit_broadcast_f32(float* destination, const float* source, int64_t count,
                         int64_t destination_stride, int batch, cuvit_stream_t stream);
 
+/* Fused attention. An extension with no single reference counterpart: it
+ * replaces the three launches of the reference's attention (vit.cu:205-245:
+ * the Q.K^T GEMM with alpha 1/sqrt(head_dim), launch_softmax in place, the
+ * weights.V GEMM) and returns bitwise the same context as that sequence run
+ * through this library, without writing the [images, heads, tokens, tokens]
+ * logits. qkv is [images, tokens, 3, heads, head_dim] (the QKV projection),
+ * context is [images, tokens, heads, head_dim]; both 16-byte aligned.
+ * Supports head_dim 64 and up to 256 tokens; other shapes are
+ * CUVIT_ERROR_INVALID_ARGUMENT (cuvit_attention_supported tells first). */
+int cuvit_attention_supported(int tokens, int head_dim);
+int cuvit_attention_f32(const float* qkv, float* context, int images, int heads, int tokens,
+                        int head_dim, cuvit_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * bfloat16 I/O twins. An extension: the reference has no reduced-precision
  * path (README.md:472-473). Storage is bf16, every reduction and every

@@ -81,9 +81,13 @@ class VisionTransformer final {
 
   private:
     void run_block(const BlockWeights& block, float* tokens, int batch, hipStream_t stream);
+    /// The reference's three attention launches (vit.cu:205-245), used when
+    /// the fused kernel does not cover the shape.
+    void attention_unfused(int batch, hipStream_t stream);
 
     VitConfig config_;
     int max_batch_ = 1;
+    bool fused_attention_ = false;
 
     DeviceArena weights_;
     DeviceArena activations_;

@@ -1,0 +1,99 @@
+"""Fused attention (an extension): softmax(Q.K^T / sqrt(64)).V per (image, head).
+
+It must equal, bit for bit, the reference's three launches (vit.cu:205-245)
+run through this library: the split-batch Q.K^T GEMM with alpha 1/8, softmax
+in place, and the weights.V GEMM into the context layout. Against the oracle
+(the reference CPU path: gemm_transposed, softmax, gemm) it is held to the
+same term-scaled tolerance as the GEMMs.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import to_device, to_host
+from numerics import require_close_scaled, require_exact
+
+pytestmark = pytest.mark.gpu
+
+HEAD_DIM = 64
+
+
+def unfused(cuvit, qkv, images, heads, tokens, device):
+    """The launcher sequence of the model's attention (vit.cu:205-245)."""
+    embed = heads * HEAD_DIM
+    row = 3 * embed
+    logits = torch.zeros(images * heads * tokens * tokens, device=device)
+    p = cuvit.gemm_problem(tokens, tokens, HEAD_DIM, cuvit.TRANSPOSED)
+    p.alpha = 1.0 / np.sqrt(np.float32(HEAD_DIM))
+    p.lda, p.ldb, p.ldc = row, row, tokens
+    b = p.batch
+    b.count, b.inner = images * heads, heads
+    b.stride_a, b.stride_b, b.stride_c = HEAD_DIM, HEAD_DIM, tokens * tokens
+    b.outer_stride_a = b.outer_stride_b = tokens * row
+    b.outer_stride_c = heads * tokens * tokens
+    cuvit.gemm(qkv, qkv[embed:], None, logits, p)
+    cuvit.softmax(logits, logits, images * heads * tokens, tokens)
+    context = torch.zeros(images * tokens * embed, device=device)
+    p = cuvit.gemm_problem(tokens, HEAD_DIM, tokens, cuvit.NO_TRANSPOSE)
+    p.lda, p.ldb, p.ldc = tokens, row, embed
+    b = p.batch
+    b.count, b.inner = images * heads, heads
+    b.stride_a, b.stride_b, b.stride_c = tokens * tokens, HEAD_DIM, HEAD_DIM
+    b.outer_stride_a = heads * tokens * tokens
+    b.outer_stride_b = tokens * row
+    b.outer_stride_c = tokens * embed
+    cuvit.gemm(logits, qkv[2 * embed:], None, context, p)
+    return context
+
+
+@pytest.mark.parametrize("images,heads,tokens", [(32, 3, 197), (2, 12, 197), (3, 2, 17), (1, 1, 1),
+                                                 (2, 3, 16), (2, 3, 65), (1, 2, 256), (4, 1, 200)])
+def test_fused_attention_is_bitwise_the_launch_sequence(cuvit, oracle, device, images, heads, tokens):
+    embed = heads * HEAD_DIM
+    qkv = to_device(oracle.generator(7000 + tokens).normal(images * tokens * 3 * embed), device)
+    expected = unfused(cuvit, qkv, images, heads, tokens, device)
+    context = torch.full((images * tokens * embed,), float("nan"), device=device)
+    cuvit.attention(qkv, context, images, heads, tokens, HEAD_DIM)
+    require_exact(to_host(context), to_host(expected),
+                  f"fused attention {images}x{heads}x{tokens} differs from the launch sequence")
+
+
+def test_fused_attention_matches_the_oracle(cuvit, oracle, device):
+    images, heads, tokens = 2, 3, 37
+    embed = heads * HEAD_DIM
+    row = 3 * embed
+    qkv = oracle.generator(7100).normal(images * tokens * row).reshape(images, tokens, 3, heads,
+                                                                          HEAD_DIM)
+    expected = np.zeros((images, tokens, heads, HEAD_DIM), np.float32)
+    scale = np.zeros_like(expected)
+    for i in range(images):
+        for h in range(heads):
+            q = np.ascontiguousarray(qkv[i, :, 0, h])
+            k = np.ascontiguousarray(qkv[i, :, 1, h])
+            v = np.ascontiguousarray(qkv[i, :, 2, h])
+            logits = oracle.gemm_transposed(q, k, None, tokens, tokens, HEAD_DIM) * np.float32(0.125)
+            weights = oracle.softmax(logits)
+            expected[i, :, h] = oracle.gemm(weights, v, None, tokens, HEAD_DIM, tokens)
+            scale[i, :, h] = oracle.gemm(np.abs(weights), np.abs(v), None, tokens, HEAD_DIM, tokens)
+    context = torch.zeros(expected.size, device=device)
+    cuvit.attention(to_device(qkv.reshape(-1), device), context, images, heads, tokens, HEAD_DIM)
+    require_close_scaled(to_host(context), expected.reshape(-1), scale.reshape(-1),
+                         "fused attention vs oracle", 1.0e-5, 1.0e-6)
+
+
+def test_fused_attention_rows_are_batch_invariant(cuvit, oracle, device):
+    """Each (image, head) gives the same bits alone as inside a batch."""
+    images, heads, tokens = 5, 3, 197
+    embed = heads * HEAD_DIM
+    per_image = tokens * 3 * embed
+    qkv = to_device(oracle.generator(7200).normal(images * per_image), device)
+    full = torch.zeros(images * tokens * embed, device=device)
+    cuvit.attention(qkv, full, images, heads, tokens, HEAD_DIM)
+    for i in (0, 3):
+        one = torch.zeros(tokens * embed, device=device)
+        cuvit.attention(qkv[i * per_image:(i + 1) * per_image].clone(), one, 1, heads, tokens, HEAD_DIM)
+        require_exact(to_host(one), to_host(full[i * tokens * embed:(i + 1) * tokens * embed]),
+                      f"image {i} differs alone")

@@ -54,6 +54,8 @@ def test_zero_extents_return_before_any_check(lib):
     assert lib.cuvit_extract_patches_f32(None, None, 0, -1, -1, -1, -1, None) == 0
     assert lib.cuvit_layer_norm_bf16(None, None, None, None, 0, 4, 1e-6, None) == 0
     assert lib.cuvit_softmax_bf16(None, None, 4, 0, None) == 0
+    assert lib.cuvit_attention_f32(None, None, 0, 3, 197, 64, None) == 0
+    assert lib.cuvit_attention_f32(None, None, 2, 3, 0, 64, None) == 0
 
 
 @pytest.mark.parametrize("call,message", [
@@ -85,6 +87,16 @@ def test_zero_extents_return_before_any_check(lib):
     (lambda l: l.cuvit_extract_patches_bf16(FAKE, None, 2, 3, 224, 224, 16, None),
      "Patch extraction operands cannot be null"),
     (lambda l: l.cuvit_gelu_bf16(FAKE, None, 3, None), "GELU operands cannot be null"),
+    (lambda l: l.cuvit_attention_f32(FAKE, FAKE, 2, -3, 197, 64, None),
+     "Attention extents cannot be negative"),
+    (lambda l: l.cuvit_attention_f32(None, FAKE, 2, 3, 197, 64, None),
+     "Attention operands cannot be null"),
+    (lambda l: l.cuvit_attention_f32(FAKE, FAKE, 2, 3, 197, 32, None),
+     "Fused attention supports head_dim 64 and at most 256 tokens"),
+    (lambda l: l.cuvit_attention_f32(FAKE, FAKE, 2, 3, 257, 64, None),
+     "Fused attention supports head_dim 64 and at most 256 tokens"),
+    (lambda l: l.cuvit_attention_f32(FAKE + 4, FAKE, 2, 3, 197, 64, None),
+     "Fused attention needs 16-byte aligned operands"),
 ])
 def test_invalid_arguments(cuvit, lib, call, message):
     status = call(lib)
@@ -102,6 +114,14 @@ def test_oversized_launches_are_length_errors(cuvit, lib):
                    lib.cuvit_extract_patches_f32(FAKE, FAKE, 1 << 20, 3, 1 << 14, 1 << 14, 16, None)):
         assert status == cuvit.ERROR_LENGTH
         assert "grid limit" in lib.cuvit_last_error().decode()
+
+
+def test_attention_shape_limits(cuvit, lib):
+    assert cuvit.attention_supported(197, 64) and cuvit.attention_supported(256, 64)
+    assert cuvit.attention_supported(1, 64)
+    assert not cuvit.attention_supported(257, 64) and not cuvit.attention_supported(197, 96)
+    assert lib.cuvit_attention_f32(FAKE, FAKE, 256, 256, 197, 64, None) == cuvit.ERROR_LENGTH
+    assert "65535" in lib.cuvit_last_error().decode()
 
 
 def gemm_status(cuvit, lib, a=FAKE, b=FAKE, c=FAKE, **fields):
