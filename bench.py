@@ -62,6 +62,23 @@ STEP_BYTES = sum(BYTES.values())
 HBM_PEAK_GBS = 8000.0
 VIT_TINY_FLOPS_PER_IMAGE = 2.507e9  # GEMM flops of one 224x224 ViT-Tiny/16 forward
 POOL_BYTES = 640 << 20  # per kernel: > 2x the 256 MB Infinity Cache
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "vit_tiny_b32_layer_kernels_hbm_traffic.md")
+
+
+def measured_traffic() -> dict:
+    """Per-launch HBM bytes (read + write) of each kernel from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary, calibrated against a plain copy
+    of known size; empty when the summary is absent. A profiler has to wrap
+    the program, so this is the last profiled run of the same code, not a
+    live figure."""
+    try:
+        with open(TRAFFIC_PROFILE) as summary:
+            for text in summary:
+                if text.startswith("traffic-bytes-json:"):
+                    return json.loads(text.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return {}
 
 
 def parse():
@@ -299,6 +316,42 @@ def counters(torch, cuvit, pools):
             launch[name](i)
             torch.cuda.synchronize()
         print(f"{name}: 3 cold launches, {BYTES[name]} algorithmic bytes each", flush=True)
+    del source, target
+    vit_base_bf16_counters(torch, cuvit, flush)
+
+
+def vit_base_bf16_counters(torch, cuvit, flush):
+    """The ViT-Base batch-64 bf16 kernels for the counter passes, three cold
+    launches each: LN [12608, 768], softmax [151296, 197] in place, the patch
+    gather [64, 3, 224, 224] and FC1 with the GELU epilogue."""
+    rows, embed, hidden, heads, batch = 64 * TOKENS, 768, 3072, 12, 64
+    bf = torch.bfloat16
+    x = torch.randn(rows * embed, device="cuda").to(bf)
+    y = torch.empty_like(x)
+    gamma = torch.ones(embed, device="cuda")
+    beta = torch.zeros(embed, device="cuda")
+    logits = torch.randn(batch * heads * TOKENS * TOKENS, device="cuda").to(bf)
+    images = torch.randn(batch * CHANNELS * IMAGE * IMAGE, device="cuda").to(bf)
+    patches = torch.empty_like(images)
+    w = (0.02 * torch.randn(hidden * embed, device="cuda")).to(bf)
+    bias = torch.zeros(hidden, device="cuda")
+    c = torch.empty(rows * hidden, device="cuda", dtype=bf)
+    problem = cuvit.gemm_problem(rows, hidden, embed, cuvit.TRANSPOSED)
+    problem.epilogue.gelu = 1
+    steps = {
+        "bf16 layer_norm [12608,768]": lambda: cuvit.layer_norm(x, gamma, beta, y, rows, embed, 1e-6),
+        "bf16 softmax [151296,197]": lambda: cuvit.softmax(logits, logits, batch * heads * TOKENS, TOKENS),
+        "bf16 extract_patches b64": lambda: cuvit.extract_patches(images, patches, batch, CHANNELS,
+                                                                  IMAGE, IMAGE, PATCH),
+        "bf16 fc1_gelu_gemm 12608x3072x768": lambda: cuvit.gemm(x, w, bias, c, problem),
+    }
+    for name, launch in steps.items():
+        for i in range(3):
+            flush.fill_(i)
+            torch.cuda.synchronize()
+            launch()
+            torch.cuda.synchronize()
+        print(f"{name}: 3 cold launches", flush=True)
 
 
 def main():
@@ -372,7 +425,8 @@ def main():
                    "bytes_per_step": STEP_BYTES, "steps_in_one_hip_graph": args.steps},
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+                     "traffic": measured_traffic().get(dominant),
+                     "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT)},
         "kernels": kernels,
     }
     model_ms = vit_forward(torch, cuvit, device, BATCH, 20)
