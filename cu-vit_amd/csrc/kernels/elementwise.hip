@@ -5,7 +5,8 @@
 //       the erf form of nn.GELU(approximate='none'); CPU path
 //       tests/reference/linear_algebra.hpp:120-129)
 // A single fp32 add rounds identically everywhere, so add is bit-exact against
-// the CPU. erff is ROCm's device libm (ocml).
+// the CPU. GELU is device_common.hpp's branch-free erfc form, shared with the
+// GEMM epilogue so both give the same bits.
 //
 // Both run as grid-stride loops over 16-byte vectors when the pointers are
 // aligned, with the tail (count % elements-per-vector) handled by the first
@@ -20,10 +21,6 @@ using namespace cuvit::device;
 
 constexpr int kBlock = 256;
 constexpr int kBlocksPerCu = 8;
-
-__device__ __forceinline__ float gelu(float x) {
-    return 0.5F * x * (1.0F + erff(x * 0.7071067811865475F));
-}
 
 __global__ __launch_bounds__(kBlock) void add_kernel(float* __restrict__ accumulator,
                                                      const float* __restrict__ addend,

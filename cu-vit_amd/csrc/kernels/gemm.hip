@@ -38,12 +38,52 @@ template <typename T> bool vector_output(const T* c, const GemmArgs& args) {
            args.stride_c % 4 == 0 && (!split || args.outer_stride_c % 4 == 0);
 }
 
+/// The px x py split of an entry's tile grid among the 8 XCDs (px * py = 8)
+/// that moves the fewest bytes into their L2 caches, A being read once per
+/// column block and B once per row block, counting B double when its block
+/// would not fit comfortably in one XCD's 4 MB L2. Measured on the ViT-Base
+/// bf16 GEMMs: FC1 183 -> 173 us, FC2 129 -> 120 us. The fp32 ViT-Tiny GEMMs
+/// (a few MB in all) gained nothing from it, so they keep row-major order.
+gemm::TileMap tile_map(const GemmArgs& args, int bm, int bn, std::size_t element) {
+    gemm::TileMap map{0, 0};
+    const int tiles_m = (args.m + bm - 1) / bm;
+    const int tiles_n = (args.n + bn - 1) / bn;
+    if (element != 2 || static_cast<std::int64_t>(tiles_m) * tiles_n < 64) {
+        return map;
+    }
+    const double a_bytes = static_cast<double>(tiles_m) * bm * args.k * element;
+    const double b_bytes = static_cast<double>(tiles_n) * bn * args.k * element;
+    constexpr double kL2Budget = 3.0 * (1 << 20);
+    double best = 0.0;
+    for (const int px : {8, 4, 2, 1}) {
+        const int py = 8 / px;
+        if (px > tiles_m || py > tiles_n) {
+            continue;
+        }
+        double cost = py * a_bytes + px * b_bytes;
+        if (b_bytes / py > kL2Budget) {
+            cost *= 2.0;
+        }
+        if (map.px == 0 || cost < best) {
+            best = cost;
+            map = gemm::TileMap{px, py};
+        }
+    }
+    return map;
+}
+
 template <typename T, int WM, int WN, int TM, int TN, int BK, bool VecA, bool VecB, bool TransB>
 hipError_t launch(const T* a, const T* b, const float* bias, T* c, const GemmArgs& args,
                   bool vector_c, hipStream_t stream) {
     using S = Shape<T, WM, WN, TM, TN, BK>;
-    const std::int64_t tiles =
-        static_cast<std::int64_t>((args.m + S::kBM - 1) / S::kBM) * ((args.n + S::kBN - 1) / S::kBN);
+    const gemm::TileMap map = tile_map(args, S::kBM, S::kBN, sizeof(T));
+    const std::int64_t tiles_m = (args.m + S::kBM - 1) / S::kBM;
+    const std::int64_t tiles_n = (args.n + S::kBN - 1) / S::kBN;
+    // With the XCD split every block gets a workgroup slot per tile of the
+    // largest block.
+    const std::int64_t tiles = map.px > 0
+                                   ? 8 * ((tiles_m + map.px - 1) / map.px) * ((tiles_n + map.py - 1) / map.py)
+                                   : tiles_m * tiles_n;
     if (tiles > 0x7FFFFFFF) {
         return hipErrorInvalidConfiguration;
     }
@@ -59,7 +99,7 @@ hipError_t launch(const T* a, const T* b, const float* bias, T* c, const GemmArg
     }
     const dim3 grid(static_cast<unsigned int>(tiles),
                     static_cast<unsigned int>(args.count < kMaxGridY ? args.count : kMaxGridY));
-    kernel<<<grid, kThreads, S::kLdsBytes, stream>>>(a, b, bias, c, args, vector_c);
+    kernel<<<grid, kThreads, S::kLdsBytes, stream>>>(a, b, bias, c, args, map, vector_c);
     return hipGetLastError();
 }
 

@@ -107,10 +107,6 @@ __device__ __forceinline__ Offsets entry_offsets(const GemmArgs& args, int entry
     return {entry * args.stride_a, entry * args.stride_b, entry * args.stride_c};
 }
 
-__device__ __forceinline__ float gelu(float x) {
-    return 0.5F * x * (1.0F + erff(x * 0.7071067811865475F));
-}
-
 /// alpha, bias, GELU: everything of the epilogue before the store.
 __device__ __forceinline__ float epilogue_value(float sum, const float* bias, int column,
                                                 const GemmArgs& args) {
@@ -224,11 +220,25 @@ template <typename T, int WM, int WN, int TM, int TN, int BK> struct Shape {
     static constexpr std::size_t kLdsBytes = 2 * kStage * sizeof(T);
 };
 
+/// Which tile a workgroup computes. With px * py == 8 the tile grid of an
+/// entry is split into px x py blocks and workgroup x goes to block x % 8:
+/// the MI355X dispatcher hands consecutive workgroups to its 8 XCDs in turn,
+/// so each XCD's L2 then serves one block, its A rows and its B columns,
+/// instead of every XCD streaming all of A. With px == 0 the tiles are in
+/// plain row-major order.
+struct TileMap {
+    int px;
+    int py;
+};
+
+/// Start of part @p i of @p n split into @p parts near-equal parts.
+__device__ __forceinline__ int split_point(int n, int parts, int i) { return n * i / parts; }
+
 template <typename T, int WM, int WN, int TM, int TN, int BK, bool VecA, bool VecB, bool TransB>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(const T* __restrict__ a,
                                                         const T* __restrict__ b,
                                                         const float* __restrict__ bias, T* c,
-                                                        GemmArgs args, bool vector_c) {
+                                                        GemmArgs args, TileMap map, bool vector_c) {
     using S = Shape<T, WM, WN, TM, TN, BK>;
     constexpr int BM = S::kBM;
     constexpr int BN = S::kBN;
@@ -247,8 +257,25 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const T* __restrict__ a,
     const int fragment_chunk = lane / E;
 
     const int tiles_n = (args.n + BN - 1) / BN;
-    const int row0 = static_cast<int>(blockIdx.x / tiles_n) * BM;
-    const int col0 = static_cast<int>(blockIdx.x % tiles_n) * BN;
+    int tile_m = static_cast<int>(blockIdx.x) / tiles_n;
+    int tile_n = static_cast<int>(blockIdx.x) % tiles_n;
+    if (map.px > 0) {
+        const int tiles_m = (args.m + BM - 1) / BM;
+        const int block = static_cast<int>(blockIdx.x) % 8;
+        const int index = static_cast<int>(blockIdx.x) / 8;
+        const int m_lo = split_point(tiles_m, map.px, block / map.py);
+        const int m_hi = split_point(tiles_m, map.px, block / map.py + 1);
+        const int n_lo = split_point(tiles_n, map.py, block % map.py);
+        const int n_hi = split_point(tiles_n, map.py, block % map.py + 1);
+        const int width = n_hi - n_lo;
+        if (index >= (m_hi - m_lo) * width) {
+            return; // this block has fewer tiles than the grid allows; no barrier is skipped
+        }
+        tile_m = m_lo + index / width;
+        tile_n = n_lo + index % width;
+    }
+    const int row0 = tile_m * BM;
+    const int col0 = tile_n * BN;
     const int steps = (args.k + BK - 1) / BK;
 
     for (int entry = blockIdx.y; entry < args.count; entry += gridDim.y) {
