@@ -19,7 +19,7 @@ roofline     the kernel with the largest share of the step: algorithmic bytes of
              a graph of back-to-back launches of that kernel over its pool.
 copy ceiling a device-to-device copy of the same bytes over the same kind of
              cold pools, per kernel: what any kernel of that size can reach.
-vit_tiny_forward  the full batch-32 forward (90 launches: attention fused) as one HIP graph.
+vit_tiny_forward  the full batch-32 forward (89 launches: attention fused, positional add in the embedding GEMM) as one HIP graph.
 vit_base_b64_bf16 the bf16 twins at ViT-Base/16 batch-64 shapes, cold.
 cpu_baseline the CPU oracle (a restatement of the reference's CPU loops) on a
              bounded sample of the same workload, one core.
@@ -434,7 +434,7 @@ def main():
         "batch": BATCH, "ms_per_forward": round(model_ms, 4),
         "images_per_s": round(BATCH / (model_ms * 1e-3), 1),
         "model_tflops": round(VIT_TINY_FLOPS_PER_IMAGE * BATCH / (model_ms * 1e-3) / 1e12, 2),
-        "launches": 90,
+        "launches": 89,
         "note": "fp32 end-to-end forward, one HIP graph, attention fused (bitwise equal to the "
                 "GEMM -> softmax -> GEMM launches); MFMA fp32 peak 157.3 TFLOP/s"}
     line["vit_base_b64_bf16"] = vit_base_bf16(torch, cuvit, device)

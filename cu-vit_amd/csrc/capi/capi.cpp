@@ -193,6 +193,21 @@ int from_hip(hipError_t result, const char* what) {
     return status;
 }
 
+int gemm_f32_with_addend(const float* a, const float* b, const float* bias, const float* addend,
+                         int ld_addend, float* c, const cuvit_gemm_problem* problem,
+                         hipStream_t stream) {
+    ResolvedGemm resolved{};
+    if (const int s = check_gemm(a, b, c, problem, &resolved); s != CUVIT_OK || resolved.empty) {
+        return s;
+    }
+    if (addend == nullptr || ld_addend < problem->n) {
+        return fail(CUVIT_ERROR_INVALID_ARGUMENT, "GEMM addend needs a row of at least n values");
+    }
+    resolved.args.addend = addend;
+    resolved.args.ld_addend = ld_addend;
+    return from_hip(detail::gemm_f32(a, b, bias, c, resolved.args, stream), "gemm launch");
+}
+
 } // namespace cuvit::capi
 
 using namespace cuvit;

@@ -25,6 +25,14 @@ int from_hip(hipError_t result, const char* what);
 /// Stores the hipError_t reported by cuvit_last_hip_error().
 void set_hip_error(int code);
 
+/// cuvit_gemm_f32 plus an [m, n] addend (row stride ld_addend, the same for
+/// every batch entry) added after the bias. Not part of the C ABI, whose
+/// problem struct is the reference's GemmProblem: the model uses it to fold
+/// the positional add into the patch-embedding GEMM.
+int gemm_f32_with_addend(const float* a, const float* b, const float* bias, const float* addend,
+                         int ld_addend, float* c, const cuvit_gemm_problem* problem,
+                         hipStream_t stream);
+
 /// Runs @p body, mapping any exception it throws to the matching status.
 template <typename Body> int guarded(Body&& body) {
     try {

@@ -10,37 +10,69 @@
 // launch with bitwise the same result and no logits buffer.
 // Around the blocks (forward, vit.cu:263-317): patch gather -> embedding GEMM
 // into rows 1.. of each image -> class token into row 0 -> positional add ->
-// blocks -> final LN -> head GEMM on the class rows only.
+// blocks -> final LN -> head GEMM on the class rows only. Here the positional
+// add rides in the embedding GEMM's epilogue and row 0 is one broadcast of
+// cls + pos[0], with the same bits as the separate launches.
 #include "cuvit/vit.hpp"
 
 #include "cuvit/capi.h"
 #include "cuvit/hip_check.hpp"
+#include "cuvit/host_buffer.hpp"
 #include "cuvit/kernels.hpp"
+
+#include "../capi/status.hpp"
 
 #include <cmath>
 #include <cstdint>
+#include <cstring>
 #include <stdexcept>
 #include <string>
+#include <utility>
 
 namespace cuvit {
 namespace {
 
 std::string block_prefix(int index) { return "blocks." + std::to_string(index) + '.'; }
 
-/// Carves space for @p name from @p arena and copies the (shape-checked)
-/// tensor into it.
-const float* upload(DeviceArena& arena, const WeightFile& file, const std::string& name,
-                    const std::vector<Extent>& extents) {
-    const float* const host = file.float_data(name, extents);
-    Extent count = 1;
-    for (const Extent e : extents) {
-        count *= e;
+/// Weights on their way to the device: each tensor is carved from the device
+/// arena and copied (shape-checked) into a pinned host mirror of the arena,
+/// and one asynchronous copy then moves the whole arena. The reference issues
+/// one synchronous cudaMemcpy per tensor (vit.cu:29-30).
+class Staging {
+  public:
+    Staging(DeviceArena& arena, std::size_t bytes) : arena_(arena), host_(bytes) {}
+
+    /// Carves @p count floats; returns the device pointer and the host mirror.
+    std::pair<float*, float*> carve(std::size_t count) {
+        float* const device = arena_.allocate_raw<float>(count);
+        const auto offset = reinterpret_cast<const std::byte*>(device) - arena_.data();
+        return {device, reinterpret_cast<float*>(host_.data() + offset)};
     }
-    float* const device = arena.allocate_raw<float>(static_cast<std::size_t>(count));
-    CUVIT_HIP_CHECK(hipMemcpy(device, host, static_cast<std::size_t>(count) * sizeof(float),
-                              hipMemcpyHostToDevice));
-    return device;
-}
+
+    const float* upload(const WeightFile& file, const std::string& name,
+                        const std::vector<Extent>& extents) {
+        const float* const source = file.float_data(name, extents);
+        Extent count = 1;
+        for (const Extent e : extents) {
+            count *= e;
+        }
+        const auto [device, mirror] = carve(static_cast<std::size_t>(count));
+        std::memcpy(mirror, source, static_cast<std::size_t>(count) * sizeof(float));
+        return device;
+    }
+
+    /// Copies everything carved so far to the device and waits for it.
+    void finish() {
+        Stream stream;
+        CUVIT_HIP_CHECK(hipMemcpyAsync(const_cast<std::byte*>(arena_.data()), host_.data(), arena_.used(),
+                                       hipMemcpyHostToDevice, stream.get()));
+        stream.synchronize();
+    }
+
+  private:
+    DeviceArena& arena_;
+    HostBuffer<std::byte> host_;
+};
 
 } // namespace
 
@@ -110,38 +142,55 @@ VisionTransformer::VisionTransformer(const VitConfig& config, const WeightFile& 
     for (const Extent count : {embed, embed, classes * embed, classes}) {
         weight_bytes += DeviceArena::reserved_bytes<float>(static_cast<std::size_t>(count));
     }
+    weight_bytes += DeviceArena::reserved_bytes<float>(static_cast<std::size_t>(embed)); // cls + pos[0]
     weights_.reserve(weight_bytes);
+    Staging staging(weights_, weight_bytes);
+    auto upload = [&](const std::string& name, const std::vector<Extent>& extents) {
+        return staging.upload(file, name, extents);
+    };
 
-    class_token_ = upload(weights_, file, "cls_token", {1, 1, embed});
-    position_embedding_ = upload(weights_, file, "pos_embed", {1, tokens, embed});
+    class_token_ = upload("cls_token", {1, 1, embed});
+    position_embedding_ = upload("pos_embed", {1, tokens, embed});
+    // Token row 0 of every image is cls + pos[0]: one fp32 add per element,
+    // the same rounding as the reference's broadcast-then-add (vit.cu:295-300).
+    {
+        const float* const cls = file.float_data("cls_token", {1, 1, embed});
+        const float* const pos = file.float_data("pos_embed", {1, tokens, embed});
+        const auto [device, mirror] = staging.carve(static_cast<std::size_t>(embed));
+        for (Extent i = 0; i < embed; ++i) {
+            mirror[i] = cls[i] + pos[i];
+        }
+        class_position_ = device;
+    }
     // The Conv2d weight [embed, C, P, P] is already the [embed, C*P*P] matrix
     // the embedding GEMM wants.
-    patch_weight_ = upload(weights_, file, "patch_embed.proj.weight",
+    patch_weight_ = upload("patch_embed.proj.weight",
                            {embed, config_.channels, config_.patch_size, config_.patch_size});
-    patch_bias_ = upload(weights_, file, "patch_embed.proj.bias", {embed});
+    patch_bias_ = upload("patch_embed.proj.bias", {embed});
 
     blocks_.resize(static_cast<std::size_t>(config_.depth));
     for (int index = 0; index < config_.depth; ++index) {
         const std::string p = block_prefix(index);
         BlockWeights& b = blocks_[static_cast<std::size_t>(index)];
-        b.norm1_gamma = upload(weights_, file, p + "norm1.weight", {embed});
-        b.norm1_beta = upload(weights_, file, p + "norm1.bias", {embed});
-        b.qkv_weight = upload(weights_, file, p + "attn.qkv.weight", {3 * embed, embed});
-        b.qkv_bias = upload(weights_, file, p + "attn.qkv.bias", {3 * embed});
-        b.proj_weight = upload(weights_, file, p + "attn.proj.weight", {embed, embed});
-        b.proj_bias = upload(weights_, file, p + "attn.proj.bias", {embed});
-        b.norm2_gamma = upload(weights_, file, p + "norm2.weight", {embed});
-        b.norm2_beta = upload(weights_, file, p + "norm2.bias", {embed});
-        b.fc1_weight = upload(weights_, file, p + "mlp.fc1.weight", {hidden, embed});
-        b.fc1_bias = upload(weights_, file, p + "mlp.fc1.bias", {hidden});
-        b.fc2_weight = upload(weights_, file, p + "mlp.fc2.weight", {embed, hidden});
-        b.fc2_bias = upload(weights_, file, p + "mlp.fc2.bias", {embed});
+        b.norm1_gamma = upload(p + "norm1.weight", {embed});
+        b.norm1_beta = upload(p + "norm1.bias", {embed});
+        b.qkv_weight = upload(p + "attn.qkv.weight", {3 * embed, embed});
+        b.qkv_bias = upload(p + "attn.qkv.bias", {3 * embed});
+        b.proj_weight = upload(p + "attn.proj.weight", {embed, embed});
+        b.proj_bias = upload(p + "attn.proj.bias", {embed});
+        b.norm2_gamma = upload(p + "norm2.weight", {embed});
+        b.norm2_beta = upload(p + "norm2.bias", {embed});
+        b.fc1_weight = upload(p + "mlp.fc1.weight", {hidden, embed});
+        b.fc1_bias = upload(p + "mlp.fc1.bias", {hidden});
+        b.fc2_weight = upload(p + "mlp.fc2.weight", {embed, hidden});
+        b.fc2_bias = upload(p + "mlp.fc2.bias", {embed});
     }
 
-    final_gamma_ = upload(weights_, file, "norm.weight", {embed});
-    final_beta_ = upload(weights_, file, "norm.bias", {embed});
-    head_weight_ = upload(weights_, file, "head.weight", {classes, embed});
-    head_bias_ = upload(weights_, file, "head.bias", {classes});
+    final_gamma_ = upload("norm.weight", {embed});
+    final_beta_ = upload("norm.bias", {embed});
+    head_weight_ = upload("head.weight", {classes, embed});
+    head_bias_ = upload("head.bias", {classes});
+    staging.finish();
 
     // Attention runs fused (no logits buffer) whenever the shape allows.
     fused_attention_ = cuvit_attention_supported(config_.token_count(), config_.head_dim()) != 0 &&
@@ -275,16 +324,19 @@ void VisionTransformer::forward(const float* images, float* logits, int batch, h
     launch_extract_patches(images, patches_, batch, config_.channels, config_.image_size,
                            config_.image_size, config_.patch_size, stream);
 
-    // Patch embeddings land in rows 1.. of each image; row 0 is the class token.
+    // Patch embeddings land in rows 1.. of each image, with the positional
+    // embedding of those rows added in the GEMM's epilogue after the bias:
+    // (sum + bias) + pos, the order of the reference's embedding GEMM followed
+    // by its positional add, so the same bits. Row 0 gets cls + pos[0].
     GemmProblem embedding =
         gemm_problem(patch_count, embed, config_.patch_elements(), GemmLayout::kTransposed);
     embedding.batch.count = batch;
     embedding.batch.stride_a = static_cast<std::int64_t>(patch_count) * config_.patch_elements();
     embedding.batch.stride_c = tokens_per_image;
-    launch_gemm(patches_, patch_weight_, patch_bias_, tokens_ + embed, embedding, stream);
-
-    launch_broadcast(tokens_, class_token_, embed, tokens_per_image, batch, stream);
-    launch_add_broadcast(tokens_, position_embedding_, tokens_per_image, batch, stream);
+    throw_on_error(capi::gemm_f32_with_addend(
+        patches_, patch_weight_, patch_bias_, position_embedding_ + embed, embed, tokens_ + embed,
+        reinterpret_cast<const cuvit_gemm_problem*>(&embedding), stream));
+    launch_broadcast(tokens_, class_position_, embed, tokens_per_image, batch, stream);
 
     for (const BlockWeights& block : blocks_) {
         run_block(block, tokens_, batch, stream);

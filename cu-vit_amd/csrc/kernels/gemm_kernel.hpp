@@ -4,7 +4,8 @@
 // src/kernels/gemm.cu:44-242):
 //   C[i][m][n] = epilogue(alpha * sum_k A[i][m][k] * B_layout[i][k][n] + bias[n])
 // where the epilogue applies, in this order, alpha, the bias, the erf GELU and
-// finally either C = value or C += value (gemm.cu:153-162). Batches are flat
+// finally either C = value or C += value (gemm.cu:153-162). Internally an
+// [m, n] addend may follow the bias (the model's positional add). Batches are flat
 // (entry * stride) or split into (entry / inner, entry % inner) with outer
 // strides (gemm.cu:58-72); every operand has its own leading dimension.
 //
@@ -107,12 +108,16 @@ __device__ __forceinline__ Offsets entry_offsets(const GemmArgs& args, int entry
     return {entry * args.stride_a, entry * args.stride_b, entry * args.stride_c};
 }
 
-/// alpha, bias, GELU: everything of the epilogue before the store.
-__device__ __forceinline__ float epilogue_value(float sum, const float* bias, int column,
+/// alpha, bias, the optional addend, GELU: everything of the epilogue before
+/// the store.
+__device__ __forceinline__ float epilogue_value(float sum, const float* bias, int row, int column,
                                                 const GemmArgs& args) {
     float value = args.alpha * sum;
     if (bias != nullptr) {
         value += bias[column];
+    }
+    if (args.addend != nullptr) {
+        value += args.addend[static_cast<std::int64_t>(row) * args.ld_addend + column];
     }
     if (args.gelu) {
         value = gelu(value);
@@ -457,7 +462,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const T* __restrict__ a,
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         value[r] = col + r < args.n
-                                       ? epilogue_value(acc[i][j][4 * q + r], bias, col + r, args)
+                                       ? epilogue_value(acc[i][j][4 * q + r], bias, row, col + r, args)
                                        : 0.F;
                     }
                     if (vector_c && col + 3 < args.n) {

@@ -59,6 +59,12 @@ struct GemmArgs {
     std::int64_t outer_stride_c;
     bool accumulate;
     bool gelu;
+    /// Optional [m, n] term added after the bias (row stride ld_addend), the
+    /// same for every batch entry; no counterpart in the reference's
+    /// GemmProblem, used by the model to fold the positional add into the
+    /// patch-embedding GEMM.
+    const float* addend = nullptr;
+    int ld_addend = 0;
 };
 
 hipError_t gemm_f32(const float* a, const float* b, const float* bias, float* c,

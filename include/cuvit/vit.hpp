@@ -94,6 +94,7 @@ class VisionTransformer final {
 
     const float* class_token_ = nullptr;
     const float* position_embedding_ = nullptr;
+    const float* class_position_ = nullptr; // cls + pos[0]
     const float* patch_weight_ = nullptr;
     const float* patch_bias_ = nullptr;
     const float* final_gamma_ = nullptr;
