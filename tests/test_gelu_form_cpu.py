@@ -1,0 +1,102 @@
+"""The GELU the kernels compute (device_common.hpp, gelu()), evaluated on the
+CPU step by step in float32, against the erf GELU in float64.
+
+The device form is erfc(z) = t * exp(-z^2 + P(t)), t = 1 / (1 + z / 2),
+z = |x| / sqrt(2), with the degree-9 polynomial P read from the header here,
+so a changed coefficient or a changed step is caught without a GPU. The GPU
+tests hold the kernels themselves to the oracle (std::erf).
+"""
+
+from __future__ import annotations
+
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+scipy_special = pytest.importorskip("scipy.special")
+
+HEADER = os.path.join(ROOT, "cu-vit_amd", "csrc", "kernels", "device_common.hpp")
+F32 = np.float32
+
+
+def coefficients():
+    """P's coefficients from the header, highest power first (Horner order)."""
+    text = open(HEADER).read()
+    body = text[text.index("__device__ __forceinline__ float gelu(float x)"):]
+    body = body[:body.index("return")]
+    first = re.search(r"float p = ([-+0-9.eE]+)F;", body).group(1)
+    rest = re.findall(r"p = fmaf\(p, t, ([-+0-9.eE]+)F\);", body)
+    return [F32(first)] + [F32(c) for c in rest]
+
+
+def fma(a, b, c):
+    # float32 fused multiply-add: the product of two float32 values is exact in
+    # float64, so one rounding of the sum to float32 remains
+    return (a.astype(np.float64) * b.astype(np.float64) + c).astype(F32)
+
+
+def device_gelu(x):
+    x = x.astype(F32)
+    z = (np.abs(x) * F32(0.70710678118654752)).astype(F32)
+    t = (1.0 / fma(F32(0.5) * np.ones_like(z), z, F32(1.0)).astype(np.float64)).astype(F32)
+    c = coefficients()
+    p = np.full_like(t, c[0])
+    for coefficient in c[1:]:
+        p = fma(p, t, np.float64(coefficient))
+    exponent = (fma(-z, z, p.astype(np.float64)) * F32(1.4426950408889634)).astype(F32)
+    erfc_z = (t * np.exp2(exponent.astype(np.float64)).astype(F32)).astype(F32)
+    half = (F32(0.5) * erfc_z).astype(F32)
+    return (x * np.where(x < 0, half, (F32(1.0) - half).astype(F32))).astype(F32)
+
+
+def exact_gelu(x):
+    x = x.astype(np.float64)
+    return 0.5 * x * scipy_special.erfc(-x / np.sqrt(2.0))
+
+
+def test_header_has_the_degree_nine_polynomial():
+    assert len(coefficients()) == 10
+
+
+def test_dense_grid_against_float64():
+    x = np.linspace(-12.0, 12.0, 400001).astype(F32)
+    error = np.abs(device_gelu(x).astype(np.float64) - exact_gelu(x))
+    assert error.max() < 5.0e-7
+    # the reference test's tolerance for GELU (elementwise_test.cu:48-49)
+    assert np.all(error <= 1.0e-6 + 1.0e-5 * np.abs(exact_gelu(x)))
+
+
+def test_landmarks_of_the_reference_test():
+    """elementwise_test.cu:38-42's landmark inputs."""
+    x = np.array([-30, -8, -2.7, -2, -1, -0.5, 0, 0.5, 1, 2, 2.7, 8, 30], F32)
+    got = device_gelu(x).astype(np.float64)
+    expected = exact_gelu(x)
+    assert np.all(np.abs(got - expected) <= 1.0e-6 + 1.0e-5 * np.abs(expected))
+    assert got[6] == 0.0 and got[-1] == 30.0
+
+
+def test_negative_tail_keeps_relative_accuracy():
+    """Where 1 + erf cancels (the textbook formula loses every digit by x = -6),
+    the erfc form stays relatively accurate; what remains is the rounding of
+    the exponent -z^2 + P(t) before exp2, about 1e-7 relative per unit of z^2."""
+    x = np.linspace(-9.0, -3.0, 20001).astype(F32)
+    expected = exact_gelu(x)
+    relative = np.abs(device_gelu(x).astype(np.float64) - expected) / np.abs(expected)
+    assert relative.max() < 1.0e-5
+
+
+def test_fit_script_reproduces_the_error_bound():
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location(
+        "gelu_fit", os.path.join(ROOT, "cu-vit_amd", "csrc", "kernels", "gelu_fit.py"))
+    module = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(module)
+    fitted, error = module.fit()
+    assert error < 5.0e-8
+    header = np.array(coefficients()[::-1], F32)  # lowest power first
+    assert np.array_equal(header, fitted.astype(F32))
