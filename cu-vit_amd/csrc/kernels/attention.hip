@@ -260,11 +260,11 @@ hipError_t attention_f32(const float* qkv, float* context, int images, int heads
     }
     const int key_tiles = (tokens + 15) / 16;
     const std::size_t lds = 2 * static_cast<std::size_t>(key_tiles) * 16 * kPitch * sizeof(float);
-    static const hipError_t opted = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(attention_kernel<kWaves>),
-        hipFuncAttributeMaxDynamicSharedMemorySize,
-        static_cast<int>(2 * 16 * kMaxKeyTiles * kPitch * sizeof(float)));
-    if (opted != hipSuccess) {
+    static std::atomic<std::uint64_t> opted_in{0};
+    if (const hipError_t opted =
+            allow_lds(reinterpret_cast<const void*>(attention_kernel<kWaves>),
+                      2 * 16 * kMaxKeyTiles * kPitch * sizeof(float), opted_in);
+        opted != hipSuccess) {
         return opted;
     }
     const dim3 grid(static_cast<unsigned int>((key_tiles + kWaves - 1) / kWaves),

@@ -88,14 +88,11 @@ hipError_t launch(const T* a, const T* b, const float* bias, T* c, const GemmArg
         return hipErrorInvalidConfiguration;
     }
     auto kernel = gemm::gemm_kernel<T, WM, WN, TM, TN, BK, VecA, VecB, TransB>;
-    if constexpr (S::kLdsBytes > 65536) {
-        // Above 64 KiB of LDS a kernel has to opt in; done once per kernel.
-        static const hipError_t opted = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-            static_cast<int>(S::kLdsBytes));
-        if (opted != hipSuccess) {
-            return opted;
-        }
+    // Above 64 KiB of LDS a kernel has to opt in, once per device.
+    static std::atomic<std::uint64_t> opted_in{0};
+    if (const hipError_t opted = allow_lds(reinterpret_cast<const void*>(kernel), S::kLdsBytes, opted_in);
+        opted != hipSuccess) {
+        return opted;
     }
     const dim3 grid(static_cast<unsigned int>(tiles),
                     static_cast<unsigned int>(args.count < kMaxGridY ? args.count : kMaxGridY));

@@ -32,6 +32,27 @@ int compute_units() {
     return units;
 }
 
+hipError_t allow_lds(const void* kernel, std::size_t bytes, std::atomic<std::uint64_t>& devices) {
+    if (bytes <= 65536) {
+        return hipSuccess;
+    }
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) {
+        return hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   static_cast<int>(bytes));
+    }
+    const std::uint64_t bit = std::uint64_t{1} << device;
+    if ((devices.load(std::memory_order_acquire) & bit) != 0) {
+        return hipSuccess;
+    }
+    const hipError_t result =
+        hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+    if (result == hipSuccess) {
+        devices.fetch_or(bit, std::memory_order_acq_rel);
+    }
+    return result;
+}
+
 unsigned int stride_grid(std::int64_t units, int units_per_block, int cap_per_cu) {
     const std::int64_t needed = (units + units_per_block - 1) / units_per_block;
     const std::int64_t cap = static_cast<std::int64_t>(compute_units()) * cap_per_cu;

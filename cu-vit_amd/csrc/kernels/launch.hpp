@@ -5,6 +5,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+#include <cstddef>
 #include <cstdint>
 
 namespace cuvit::detail {
@@ -81,6 +83,11 @@ hipError_t attention_f32(const float* qkv, float* context, int images, int heads
 
 // Device facts used to shape grids, cached per device.
 int compute_units();
+
+/// Lets @p kernel use @p bytes of dynamic LDS (an opt-in above 64 KiB) on the
+/// current device, once per device; @p devices is the kernel's own bit set of
+/// the devices already done.
+hipError_t allow_lds(const void* kernel, std::size_t bytes, std::atomic<std::uint64_t>& devices);
 
 /// Grid size for a grid-stride kernel: enough blocks to cover @p units of work,
 /// capped so the work-item count stays far inside the 32-bit dispatch limit.

@@ -160,3 +160,41 @@ def test_softmax_bf16_paths_agree_bitwise(cuvit, oracle, device):
         cuvit.softmax(part, part, 5, columns)
         require_exact(bf16_bits(part).reshape(5, columns), full[start:start + 5],
                       f"bf16 rows {start}.. differ between paths")
+
+
+@pytest.mark.parametrize("m,n,k,layout", [(2000, 1100, 96, 1), (1500, 2100, 72, 0), (4100, 1030, 40, 1)])
+def test_gemm_bf16_tile_blocks_per_xcd(cuvit, oracle, device, m, n, k, layout):
+    """Enough tiles for the XCD block order, with block splits that do not
+    divide the tile grid evenly; every output must be produced exactly once."""
+    a_bits, a = bf16_inputs(oracle, m + 3 * n, m * k)
+    b_bits, b = bf16_inputs(oracle, m + 5 * k, n * k)
+    bias = oracle.generator(9).normal(n)
+    if layout == 1:
+        expected = oracle.gemm_transposed(a, b, bias, m, n, k)
+    else:
+        expected = oracle.gemm(a, b, bias, m, n, k)
+    scale = oracle.term_magnitudes(a, b, m, n, k, layout == 1)
+    c = torch.full((m * n,), float("nan"), dtype=torch.bfloat16, device=device)
+    cuvit.gemm(bf16_tensor(a_bits, device), bf16_tensor(b_bits, device), to_device(bias, device), c,
+               cuvit.gemm_problem(m, n, k, layout))
+    require_gemm_close(bf16_to_float(bf16_bits(c)).reshape(m, n), expected, scale,
+                       f"bf16 GEMM {m}x{n}x{k} in XCD blocks")
+
+
+def test_gemm_bf16_batched_tile_blocks(cuvit, oracle, device):
+    """Batched entries (grid rows) each split into XCD blocks."""
+    count, m, n, k = 3, 700, 600, 48
+    a_bits, a = bf16_inputs(oracle, 61, count * m * k)
+    b_bits, b = bf16_inputs(oracle, 62, count * n * k)
+    c = torch.full((count * m * n,), float("nan"), dtype=torch.bfloat16, device=device)
+    problem = cuvit.gemm_problem(m, n, k, 1)
+    problem.batch.count = count
+    problem.batch.stride_a, problem.batch.stride_b, problem.batch.stride_c = m * k, n * k, m * n
+    cuvit.gemm(bf16_tensor(a_bits, device), bf16_tensor(b_bits, device), None, c, problem)
+    actual = bf16_to_float(bf16_bits(c)).reshape(count, m, n)
+    for e in range(count):
+        ae = a.reshape(count, m * k)[e]
+        be = b.reshape(count, n * k)[e]
+        expected = oracle.gemm_transposed(ae, be, None, m, n, k)
+        scale = oracle.term_magnitudes(ae, be, m, n, k, True)
+        require_gemm_close(actual[e], expected, scale, f"bf16 batched entry {e}")
