@@ -20,6 +20,7 @@ roofline     the kernel with the largest share of the step: algorithmic bytes of
 copy ceiling a device-to-device copy of the same bytes over the same kind of
              cold pools, per kernel: what any kernel of that size can reach.
 vit_tiny_forward  the full batch-32 forward (89 launches: attention fused, positional add in the embedding GEMM) as one HIP graph.
+vit_*_forward_bf16 the bf16 model: ViT-Tiny at batch 32 and ViT-Base at batch 64.
 vit_base_b64_bf16 the bf16 twins at ViT-Base/16 batch-64 shapes, cold.
 cpu_baseline the CPU oracle (a restatement of the reference's CPU loops) on a
              bounded sample of the same workload, one core.
@@ -60,7 +61,6 @@ BYTES = {
 }
 STEP_BYTES = sum(BYTES.values())
 HBM_PEAK_GBS = 8000.0
-VIT_TINY_FLOPS_PER_IMAGE = 2.507e9  # GEMM flops of one 224x224 ViT-Tiny/16 forward
 POOL_BYTES = 640 << 20  # per kernel: > 2x the 256 MB Infinity Cache
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "vit_tiny_b32_layer_kernels_hbm_traffic.md")
 
@@ -181,32 +181,53 @@ def copy_ceiling(torch, device, nbytes: int) -> float:
     return ms
 
 
-def vit_forward(torch, cuvit, device, batch: int, replays: int):
-    """ms per ViT-Tiny/16 forward at @p batch (random N(0, 0.02) weights, LN
-    gamma N(1, 0.02), written as a .cvw file and loaded), one HIP graph."""
+def vit_config(cuvit, base: bool):
+    """ViT-Tiny/16 (VitConfig's defaults) or ViT-Base/16 (E 768, 12 heads, MLP 3072)."""
+    config = cuvit.default_config()
+    if base:
+        config.embed_dim, config.heads, config.mlp_hidden = 768, 12, 3072
+    return config
+
+
+def vit_gemm_flops(config) -> float:
+    """GEMM flops of one image's forward: embedding, per block QKV, Q.K^T,
+    weights.V, projection, FC1, FC2, and the head."""
+    e, hidden, classes = config.embed_dim, config.mlp_hidden, config.classes
+    patches = (config.image_size // config.patch_size) ** 2
+    tokens = patches + 1
+    block = 2.0 * tokens * e * (3 * e + e + 2 * hidden) + 4.0 * tokens * tokens * e
+    return 2.0 * patches * e * config.channels * config.patch_size ** 2 + config.depth * block \
+        + 2.0 * e * classes
+
+
+def vit_forward(torch, cuvit, device, batch: int, replays: int, base: bool = False,
+                precision: int = 0):
+    """ms per ViT/16 forward at @p batch (random N(0, 0.02) weights, LN gamma
+    N(1, 0.02), written as a .cvw file and loaded), one HIP graph."""
     import tempfile
 
     import numpy as np
 
-    config = cuvit.default_config()
+    config = vit_config(cuvit, base)
     rng = np.random.default_rng(404)
     writer = cuvit.WeightWriter()
     for name, shape in cuvit.expected_tensor_names(config):
         mean = 1.0 if name.endswith(("norm1.weight", "norm2.weight")) or name == "norm.weight" else 0.0
-        writer.add(name, (mean + 0.02 * rng.standard_normal(shape)).astype(np.float32))
+        writer.add(name, (mean + 0.02 * rng.standard_normal(shape, dtype=np.float32)).astype(np.float32))
     with tempfile.TemporaryDirectory() as folder:
-        path = os.path.join(folder, "vit_tiny.cvw")
+        path = os.path.join(folder, "vit.cvw")
         writer.write(path)
         writer.close()
         weights = cuvit.WeightFile(path)
-        model = cuvit.VisionTransformer(config, weights, batch)
+        model = cuvit.VisionTransformer(config, weights, batch, precision)
+        weights.close()
     images = torch.rand(batch * CHANNELS * IMAGE * IMAGE, device=device) * 2 - 1
     logits = torch.empty(batch * config.classes, device=device)
     model.forward(images, logits, batch)
     torch.cuda.synchronize()
     ms = timed_graph(torch, lambda: model.forward(images, logits, batch), replays)
     model.close()
-    return ms
+    return ms, vit_gemm_flops(config)
 
 
 def vit_base_bf16(torch, cuvit, device):
@@ -429,14 +450,24 @@ def main():
                      "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT)},
         "kernels": kernels,
     }
-    model_ms = vit_forward(torch, cuvit, device, BATCH, 20)
+    model_ms, flops = vit_forward(torch, cuvit, device, BATCH, 20)
     line["vit_tiny_forward"] = {
         "batch": BATCH, "ms_per_forward": round(model_ms, 4),
         "images_per_s": round(BATCH / (model_ms * 1e-3), 1),
-        "model_tflops": round(VIT_TINY_FLOPS_PER_IMAGE * BATCH / (model_ms * 1e-3) / 1e12, 2),
+        "model_tflops": round(flops * BATCH / (model_ms * 1e-3) / 1e12, 2),
         "launches": 89,
         "note": "fp32 end-to-end forward, one HIP graph, attention fused (bitwise equal to the "
                 "GEMM -> softmax -> GEMM launches); MFMA fp32 peak 157.3 TFLOP/s"}
+    for key, base, batch in (("vit_tiny_forward_bf16", False, BATCH),
+                             ("vit_base_forward_bf16", True, 64)):
+        model_ms, flops = vit_forward(torch, cuvit, device, batch, 10, base=base,
+                                      precision=cuvit.PRECISION_BF16)
+        line[key] = {
+            "batch": batch, "ms_per_forward": round(model_ms, 4),
+            "images_per_s": round(batch / (model_ms * 1e-3), 1),
+            "model_tflops": round(flops * batch / (model_ms * 1e-3) / 1e12, 2),
+            "note": "bf16 weights and activations, fp32 reductions, one HIP graph, attention "
+                    "unfused (GEMM -> softmax -> GEMM); MFMA bf16 dense peak 2.5 PFLOP/s"}
     line["vit_base_b64_bf16"] = vit_base_bf16(torch, cuvit, device)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -85,6 +85,24 @@ int check_gelu(const void* input, const void* output, std::int64_t count, bool* 
     return ok();
 }
 
+int check_broadcast(const void* destination, const void* source, std::int64_t count,
+                    std::int64_t destination_stride, int batch, bool* empty) {
+    *empty = count == 0 || batch == 0;
+    if (*empty) {
+        return ok();
+    }
+    if (count < 0 || batch < 0 || destination_stride < count) {
+        return fail(CUVIT_ERROR_INVALID_ARGUMENT, "Broadcast extents are inconsistent");
+    }
+    if (destination == nullptr || source == nullptr) {
+        return fail(CUVIT_ERROR_INVALID_ARGUMENT, "Broadcast operands cannot be null");
+    }
+    if (exceeds_grid(saturating_product(count, batch))) {
+        return grid_error();
+    }
+    return ok();
+}
+
 int check_patches(const void* images, const void* patches, int batch, int channels, int height,
                   int width, int patch, bool* empty) {
     *empty = batch == 0;
@@ -206,6 +224,21 @@ int gemm_f32_with_addend(const float* a, const float* b, const float* bias, cons
     resolved.args.addend = addend;
     resolved.args.ld_addend = ld_addend;
     return from_hip(detail::gemm_f32(a, b, bias, c, resolved.args, stream), "gemm launch");
+}
+
+int gemm_bf16_with_addend(const std::uint16_t* a, const std::uint16_t* b, const float* bias,
+                          const float* addend, int ld_addend, std::uint16_t* c,
+                          const cuvit_gemm_problem* problem, hipStream_t stream) {
+    ResolvedGemm resolved{};
+    if (const int s = check_gemm(a, b, c, problem, &resolved); s != CUVIT_OK || resolved.empty) {
+        return s;
+    }
+    if (addend == nullptr || ld_addend < problem->n) {
+        return fail(CUVIT_ERROR_INVALID_ARGUMENT, "GEMM addend needs a row of at least n values");
+    }
+    resolved.args.addend = addend;
+    resolved.args.ld_addend = ld_addend;
+    return from_hip(detail::gemm_bf16(a, b, bias, c, resolved.args, stream), "gemm launch");
 }
 
 } // namespace cuvit::capi
@@ -392,21 +425,48 @@ int cuvit_attention_f32(const float* qkv, float* context, int images, int heads,
 
 int cuvit_broadcast_f32(float* destination, const float* source, int64_t count,
                         int64_t destination_stride, int batch, cuvit_stream_t stream) {
-    if (count == 0 || batch == 0) {
-        return capi::ok();
-    }
-    if (count < 0 || batch < 0 || destination_stride < count) {
-        return capi::fail(CUVIT_ERROR_INVALID_ARGUMENT, "Broadcast extents are inconsistent");
-    }
-    if (destination == nullptr || source == nullptr) {
-        return capi::fail(CUVIT_ERROR_INVALID_ARGUMENT, "Broadcast operands cannot be null");
-    }
-    if (capi::exceeds_grid(capi::saturating_product(count, batch))) {
-        return capi::grid_error();
+    bool empty = false;
+    if (const int s = capi::check_broadcast(destination, source, count, destination_stride, batch,
+                                            &empty);
+        s != CUVIT_OK || empty) {
+        return s;
     }
     return from_hip(detail::broadcast_f32(destination, source, count, destination_stride, batch,
                                           capi::as_hip(stream)),
                     "broadcast launch");
+}
+
+int cuvit_broadcast_bf16(cuvit_bf16* destination, const cuvit_bf16* source, int64_t count,
+                         int64_t destination_stride, int batch, cuvit_stream_t stream) {
+    bool empty = false;
+    if (const int s = capi::check_broadcast(destination, source, count, destination_stride, batch,
+                                            &empty);
+        s != CUVIT_OK || empty) {
+        return s;
+    }
+    return from_hip(detail::broadcast_bf16(destination, source, count, destination_stride, batch,
+                                           capi::as_hip(stream)),
+                    "broadcast launch");
+}
+
+int cuvit_convert_f32_to_bf16(const float* input, cuvit_bf16* output, int64_t count,
+                              cuvit_stream_t stream) {
+    bool empty = false;
+    if (const int s = capi::check_gelu(input, output, count, &empty); s != CUVIT_OK || empty) {
+        return s;
+    }
+    return from_hip(detail::convert_f32_to_bf16(input, output, count, capi::as_hip(stream)),
+                    "convert launch");
+}
+
+int cuvit_convert_bf16_to_f32(const cuvit_bf16* input, float* output, int64_t count,
+                              cuvit_stream_t stream) {
+    bool empty = false;
+    if (const int s = capi::check_gelu(input, output, count, &empty); s != CUVIT_OK || empty) {
+        return s;
+    }
+    return from_hip(detail::convert_bf16_to_f32(input, output, count, capi::as_hip(stream)),
+                    "convert launch");
 }
 
 int cuvit_gemm_f32(const float* a, const float* b, const float* bias, float* c,

@@ -149,16 +149,34 @@ int cuvit_vit_config_validate(const cuvit_vit_config* config) {
 
 int cuvit_vit_create(const cuvit_vit_config* config, const cuvit_weight_file* file, int max_batch,
                      cuvit_vit** model) {
+    return cuvit_vit_create_ex(config, file, max_batch, CUVIT_PRECISION_F32, model);
+}
+
+int cuvit_vit_create_ex(const cuvit_vit_config* config, const cuvit_weight_file* file,
+                        int max_batch, int precision, cuvit_vit** model) {
     return guarded([&]() -> int {
         if (config == nullptr || file == nullptr || model == nullptr) {
             return fail(CUVIT_ERROR_INVALID_ARGUMENT, "config, file and out-pointer cannot be null");
         }
+        if (precision != CUVIT_PRECISION_F32 && precision != CUVIT_PRECISION_BF16) {
+            return fail(CUVIT_ERROR_INVALID_ARGUMENT, "precision is not a cuvit_precision value");
+        }
         auto created = std::make_unique<cuvit_vit>();
-        created->model =
-            std::make_unique<cuvit::VisionTransformer>(to_config(*config), file->file, max_batch);
+        created->model = std::make_unique<cuvit::VisionTransformer>(
+            to_config(*config), file->file, max_batch,
+            precision == CUVIT_PRECISION_BF16 ? cuvit::Precision::kBFloat16
+                                              : cuvit::Precision::kFloat32);
         *model = created.release();
         return CUVIT_OK;
     });
+}
+
+int cuvit_vit_precision(const cuvit_vit* model) {
+    if (model == nullptr) {
+        return -1;
+    }
+    return model->model->precision() == cuvit::Precision::kBFloat16 ? CUVIT_PRECISION_BF16
+                                                                    : CUVIT_PRECISION_F32;
 }
 
 int cuvit_vit_forward(cuvit_vit* model, const float* images, float* logits, int batch,

@@ -7,6 +7,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <new>
 #include <stdexcept>
 #include <string>
@@ -32,6 +33,12 @@ void set_hip_error(int code);
 int gemm_f32_with_addend(const float* a, const float* b, const float* bias, const float* addend,
                          int ld_addend, float* c, const cuvit_gemm_problem* problem,
                          hipStream_t stream);
+
+/// gemm_f32_with_addend's bf16 twin: bf16 A, B and C, fp32 bias and addend,
+/// one rounding at the store.
+int gemm_bf16_with_addend(const std::uint16_t* a, const std::uint16_t* b, const float* bias,
+                          const float* addend, int ld_addend, std::uint16_t* c,
+                          const cuvit_gemm_problem* problem, hipStream_t stream);
 
 /// Runs @p body, mapping any exception it throws to the matching status.
 template <typename Body> int guarded(Body&& body) {

@@ -122,4 +122,10 @@ void launch_extract_patches(const std::uint16_t* images, std::uint16_t* patches,
                                               patch, as_c(stream)));
 }
 
+void launch_broadcast(std::uint16_t* destination, const std::uint16_t* source, std::int64_t count,
+                      std::int64_t destination_stride, int batch, hipStream_t stream) {
+    throw_on_error(
+        cuvit_broadcast_bf16(destination, source, count, destination_stride, batch, as_c(stream)));
+}
+
 } // namespace cuvit

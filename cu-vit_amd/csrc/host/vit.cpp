@@ -26,13 +26,35 @@
 #include <cstdint>
 #include <cstring>
 #include <stdexcept>
+#include <iterator>
 #include <string>
+#include <type_traits>
 #include <utility>
 
 namespace cuvit {
 namespace {
 
 std::string block_prefix(int index) { return "blocks." + std::to_string(index) + '.'; }
+
+Extent element_count(const std::vector<Extent>& extents) {
+    Extent count = 1;
+    for (const Extent e : extents) {
+        count *= e;
+    }
+    return count;
+}
+
+/// bf16 bits of @p value, rounded to nearest with ties to even; a NaN stays a
+/// quiet NaN. The rounding of the kernels' stores (v_cvt_pk_bf16_f32).
+std::uint16_t round_to_bf16(float value) {
+    std::uint32_t bits = 0;
+    std::memcpy(&bits, &value, sizeof(bits));
+    if ((bits & 0x7F800000U) == 0x7F800000U && (bits & 0x007FFFFFU) != 0) {
+        return static_cast<std::uint16_t>((bits >> 16) | 0x0040U);
+    }
+    bits += 0x7FFFU + ((bits >> 16) & 1U);
+    return static_cast<std::uint16_t>(bits >> 16);
+}
 
 /// Weights on their way to the device: each tensor is carved from the device
 /// arena and copied (shape-checked) into a pinned host mirror of the arena,
@@ -42,22 +64,28 @@ class Staging {
   public:
     Staging(DeviceArena& arena, std::size_t bytes) : arena_(arena), host_(bytes) {}
 
-    /// Carves @p count floats; returns the device pointer and the host mirror.
-    std::pair<float*, float*> carve(std::size_t count) {
-        float* const device = arena_.allocate_raw<float>(count);
+    /// Carves @p count elements; returns the device pointer and the host mirror.
+    template <typename T> std::pair<T*, T*> carve(std::size_t count) {
+        T* const device = arena_.allocate_raw<T>(count);
         const auto offset = reinterpret_cast<const std::byte*>(device) - arena_.data();
-        return {device, reinterpret_cast<float*>(host_.data() + offset)};
+        return {device, reinterpret_cast<T*>(host_.data() + offset)};
     }
 
-    const float* upload(const WeightFile& file, const std::string& name,
-                        const std::vector<Extent>& extents) {
+    /// Stages tensor @p name in storage type T: copied as fp32, or rounded
+    /// to bf16 bits.
+    template <typename T>
+    const T* upload(const WeightFile& file, const std::string& name,
+                    const std::vector<Extent>& extents) {
         const float* const source = file.float_data(name, extents);
-        Extent count = 1;
-        for (const Extent e : extents) {
-            count *= e;
+        const auto count = static_cast<std::size_t>(element_count(extents));
+        const auto [device, mirror] = carve<T>(count);
+        if constexpr (std::is_same_v<T, float>) {
+            std::memcpy(mirror, source, count * sizeof(float));
+        } else {
+            for (std::size_t i = 0; i < count; ++i) {
+                mirror[i] = round_to_bf16(source[i]);
+            }
         }
-        const auto [device, mirror] = carve(static_cast<std::size_t>(count));
-        std::memcpy(mirror, source, static_cast<std::size_t>(count) * sizeof(float));
         return device;
     }
 
@@ -73,6 +101,25 @@ class Staging {
     DeviceArena& arena_;
     HostBuffer<std::byte> host_;
 };
+
+// Launch overloads by storage type. fp32 and bf16 share the launchers of
+// cuvit/kernels.hpp; the rest go through the C ABI.
+void gemm_with_addend(const float* a, const float* b, const float* bias, const float* addend,
+                      int ld_addend, float* c, const GemmProblem& problem, hipStream_t stream) {
+    throw_on_error(capi::gemm_f32_with_addend(a, b, bias, addend, ld_addend, c,
+                                              reinterpret_cast<const cuvit_gemm_problem*>(&problem),
+                                              stream));
+}
+
+void gemm_with_addend(const std::uint16_t* a, const std::uint16_t* b, const float* bias,
+                      const float* addend, int ld_addend, std::uint16_t* c,
+                      const GemmProblem& problem, hipStream_t stream) {
+    throw_on_error(capi::gemm_bf16_with_addend(a, b, bias, addend, ld_addend, c,
+                                               reinterpret_cast<const cuvit_gemm_problem*>(&problem),
+                                               stream));
+}
+
+cuvit_stream_t as_c(hipStream_t stream) { return reinterpret_cast<cuvit_stream_t>(stream); }
 
 } // namespace
 
@@ -111,114 +158,179 @@ std::size_t VisionTransformer::image_elements() const noexcept {
     return static_cast<std::size_t>(config_.channels) * config_.image_size * config_.image_size;
 }
 
-VisionTransformer::VisionTransformer(const VitConfig& config, const WeightFile& file, int max_batch)
-    : config_(config), max_batch_(max_batch) {
+VisionTransformer::VisionTransformer(const VitConfig& config, const WeightFile& file, int max_batch,
+                                     Precision precision)
+    : config_(config), max_batch_(max_batch), precision_(precision) {
     config_.validate();
     if (max_batch_ < 1) {
         throw std::invalid_argument("The maximum batch size must be at least one");
     }
+    if (precision_ != Precision::kFloat32 && precision_ != Precision::kBFloat16) {
+        throw std::invalid_argument("Unknown model precision");
+    }
+    if (precision_ == Precision::kFloat32) {
+        load(file, f32_);
+        reserve_activations(f32_);
+    } else {
+        load(file, bf16_);
+        reserve_activations(bf16_);
+    }
+}
 
+template <typename T> void VisionTransformer::load(const WeightFile& file, Stored<T>& stored) {
+    constexpr bool kFloat = std::is_same_v<T, float>;
     const Extent embed = config_.embed_dim;
     const Extent tokens = config_.token_count();
-    const Extent patches = config_.patch_count();
     const Extent hidden = config_.mlp_hidden;
     const Extent patch_elements = config_.patch_elements();
     const Extent classes = config_.classes;
 
     // The weight arena is sized from the configuration, not from the file, so
-    // extra tensors in a file cost nothing.
-    const std::vector<Extent> per_block = {embed,         embed, 3 * embed * embed, 3 * embed,
-                                           embed * embed, embed, embed,             embed,
-                                           hidden * embed, hidden, embed * hidden,  embed};
+    // extra tensors in a file cost nothing. Vectors are fp32; the GEMM
+    // matrices and the class row are in storage type T.
     std::size_t weight_bytes = 0;
-    for (const Extent count : {embed, tokens * embed, embed * patch_elements, embed}) {
+    auto vector = [&](Extent count) {
         weight_bytes += DeviceArena::reserved_bytes<float>(static_cast<std::size_t>(count));
-    }
+    };
+    auto matrix = [&](Extent count) {
+        weight_bytes += DeviceArena::reserved_bytes<T>(static_cast<std::size_t>(count));
+    };
+    vector(embed);          // cls
+    vector(tokens * embed); // pos
+    matrix(embed * patch_elements);
+    vector(embed);
     for (int block = 0; block < config_.depth; ++block) {
-        for (const Extent count : per_block) {
-            weight_bytes += DeviceArena::reserved_bytes<float>(static_cast<std::size_t>(count));
-        }
+        vector(embed);
+        vector(embed);
+        matrix(3 * embed * embed);
+        vector(3 * embed);
+        matrix(embed * embed);
+        vector(embed);
+        vector(embed);
+        vector(embed);
+        matrix(hidden * embed);
+        vector(hidden);
+        matrix(embed * hidden);
+        vector(embed);
     }
-    for (const Extent count : {embed, embed, classes * embed, classes}) {
-        weight_bytes += DeviceArena::reserved_bytes<float>(static_cast<std::size_t>(count));
-    }
-    weight_bytes += DeviceArena::reserved_bytes<float>(static_cast<std::size_t>(embed)); // cls + pos[0]
+    vector(embed);
+    vector(embed);
+    matrix(classes * embed);
+    vector(classes);
+    matrix(embed); // cls + pos[0]
     weights_.reserve(weight_bytes);
+
     Staging staging(weights_, weight_bytes);
     auto upload = [&](const std::string& name, const std::vector<Extent>& extents) {
-        return staging.upload(file, name, extents);
+        return staging.upload<float>(file, name, extents);
+    };
+    auto upload_matrix = [&](const std::string& name, const std::vector<Extent>& extents) {
+        return staging.upload<T>(file, name, extents);
     };
 
     class_token_ = upload("cls_token", {1, 1, embed});
     position_embedding_ = upload("pos_embed", {1, tokens, embed});
-    // Token row 0 of every image is cls + pos[0]: one fp32 add per element,
-    // the same rounding as the reference's broadcast-then-add (vit.cu:295-300).
-    {
-        const float* const cls = file.float_data("cls_token", {1, 1, embed});
-        const float* const pos = file.float_data("pos_embed", {1, tokens, embed});
-        const auto [device, mirror] = staging.carve(static_cast<std::size_t>(embed));
-        for (Extent i = 0; i < embed; ++i) {
-            mirror[i] = cls[i] + pos[i];
-        }
-        class_position_ = device;
-    }
     // The Conv2d weight [embed, C, P, P] is already the [embed, C*P*P] matrix
     // the embedding GEMM wants.
-    patch_weight_ = upload("patch_embed.proj.weight",
-                           {embed, config_.channels, config_.patch_size, config_.patch_size});
+    stored.patch_weight = upload_matrix(
+        "patch_embed.proj.weight", {embed, config_.channels, config_.patch_size, config_.patch_size});
     patch_bias_ = upload("patch_embed.proj.bias", {embed});
 
-    blocks_.resize(static_cast<std::size_t>(config_.depth));
+    blocks_.assign(static_cast<std::size_t>(config_.depth), BlockWeights{});
+    stored.blocks.assign(static_cast<std::size_t>(config_.depth), typename Stored<T>::Matrices{});
     for (int index = 0; index < config_.depth; ++index) {
         const std::string p = block_prefix(index);
         BlockWeights& b = blocks_[static_cast<std::size_t>(index)];
+        typename Stored<T>::Matrices& m = stored.blocks[static_cast<std::size_t>(index)];
         b.norm1_gamma = upload(p + "norm1.weight", {embed});
         b.norm1_beta = upload(p + "norm1.bias", {embed});
-        b.qkv_weight = upload(p + "attn.qkv.weight", {3 * embed, embed});
+        m.qkv = upload_matrix(p + "attn.qkv.weight", {3 * embed, embed});
         b.qkv_bias = upload(p + "attn.qkv.bias", {3 * embed});
-        b.proj_weight = upload(p + "attn.proj.weight", {embed, embed});
+        m.proj = upload_matrix(p + "attn.proj.weight", {embed, embed});
         b.proj_bias = upload(p + "attn.proj.bias", {embed});
         b.norm2_gamma = upload(p + "norm2.weight", {embed});
         b.norm2_beta = upload(p + "norm2.bias", {embed});
-        b.fc1_weight = upload(p + "mlp.fc1.weight", {hidden, embed});
+        m.fc1 = upload_matrix(p + "mlp.fc1.weight", {hidden, embed});
         b.fc1_bias = upload(p + "mlp.fc1.bias", {hidden});
-        b.fc2_weight = upload(p + "mlp.fc2.weight", {embed, hidden});
+        m.fc2 = upload_matrix(p + "mlp.fc2.weight", {embed, hidden});
         b.fc2_bias = upload(p + "mlp.fc2.bias", {embed});
+        if constexpr (kFloat) {
+            b.qkv_weight = m.qkv;
+            b.proj_weight = m.proj;
+            b.fc1_weight = m.fc1;
+            b.fc2_weight = m.fc2;
+        }
     }
 
     final_gamma_ = upload("norm.weight", {embed});
     final_beta_ = upload("norm.bias", {embed});
-    head_weight_ = upload("head.weight", {classes, embed});
+    stored.head_weight = upload_matrix("head.weight", {classes, embed});
     head_bias_ = upload("head.bias", {classes});
-    staging.finish();
+    if constexpr (kFloat) {
+        patch_weight_ = stored.patch_weight;
+        head_weight_ = stored.head_weight;
+    }
 
-    // Attention runs fused (no logits buffer) whenever the shape allows.
-    fused_attention_ = cuvit_attention_supported(config_.token_count(), config_.head_dim()) != 0 &&
+    // Token row 0 of every image is cls + pos[0]: one fp32 add per element,
+    // the same rounding as the reference's broadcast-then-add (vit.cu:295-300),
+    // then (bf16) one rounding to storage, as every other stored token.
+    {
+        const float* const cls = file.float_data("cls_token", {1, 1, embed});
+        const float* const pos = file.float_data("pos_embed", {1, tokens, embed});
+        const auto [device, mirror] = staging.carve<T>(static_cast<std::size_t>(embed));
+        for (Extent i = 0; i < embed; ++i) {
+            const float sum = cls[i] + pos[i];
+            if constexpr (kFloat) {
+                mirror[i] = sum;
+            } else {
+                mirror[i] = round_to_bf16(sum);
+            }
+        }
+        stored.class_position = device;
+    }
+    staging.finish();
+}
+
+template <typename T> void VisionTransformer::reserve_activations(Stored<T>& stored) {
+    constexpr bool kFloat = std::is_same_v<T, float>;
+    // Attention runs fused (fp32, no logits buffer) whenever the shape allows.
+    fused_attention_ = kFloat &&
+                       cuvit_attention_supported(config_.token_count(), config_.head_dim()) != 0 &&
                        static_cast<std::int64_t>(max_batch_) * config_.heads <= 65535;
 
-    // Activation scratch for max_batch images, shared by every block.
     const Extent images = max_batch_;
-    const Extent activation_counts[] = {
-        images * patches * patch_elements,        // patch matrix
-        images * tokens * embed,                  // residual stream
-        images * tokens * embed,                  // normalized
-        images * tokens * 3 * embed,              // packed q, k, v
-        fused_attention_ ? 0 : images * config_.heads * tokens * tokens, // attention logits
-        images * tokens * embed,                  // attention context
-        images * tokens * hidden,                 // MLP hidden
+    const Extent embed = config_.embed_dim;
+    const Extent tokens = config_.token_count();
+    const Extent hidden = config_.mlp_hidden;
+    // Activation scratch for max_batch images, shared by every block.
+    const Extent counts[] = {
+        kFloat ? 0 : images * static_cast<Extent>(image_elements()),          // input in bf16
+        images * config_.patch_count() * config_.patch_elements(),           // patch matrix
+        images * tokens * embed,                                              // residual stream
+        images * tokens * embed,                                              // normalized
+        images * tokens * 3 * embed,                                          // packed q, k, v
+        fused_attention_ ? 0 : images * config_.heads * tokens * tokens,      // attention logits
+        images * tokens * embed,                                              // attention context
+        images * tokens * hidden,                                             // MLP hidden
+        kFloat ? 0 : images * config_.classes,                                // logits in bf16
     };
-    std::size_t activation_bytes = 0;
-    for (const Extent count : activation_counts) {
-        activation_bytes += DeviceArena::reserved_bytes<float>(static_cast<std::size_t>(count));
+    std::size_t bytes = 0;
+    for (const Extent count : counts) {
+        bytes += DeviceArena::reserved_bytes<T>(static_cast<std::size_t>(count));
     }
-    activations_.reserve(activation_bytes);
-    float** const slots[] = {&patches_, &tokens_, &normalized_, &qkv_, &attention_, &context_, &hidden_};
-    for (std::size_t i = 0; i < 7; ++i) {
-        *slots[i] = activations_.allocate_raw<float>(static_cast<std::size_t>(activation_counts[i]));
+    activations_.reserve(bytes);
+    T** const slots[] = {&stored.images, &stored.patches,   &stored.tokens,
+                         &stored.normalized, &stored.qkv,   &stored.attention,
+                         &stored.context,    &stored.hidden, &stored.logits};
+    static_assert(std::size(slots) == std::size(counts));
+    for (std::size_t i = 0; i < std::size(slots); ++i) {
+        *slots[i] = counts[i] == 0 ? nullptr
+                                   : activations_.allocate_raw<T>(static_cast<std::size_t>(counts[i]));
     }
 }
 
-void VisionTransformer::attention_unfused(int batch, hipStream_t stream) {
+template <typename T>
+void VisionTransformer::attention_unfused(Stored<T>& stored, int batch, hipStream_t stream) {
     const int token_count = config_.token_count();
     const int embed = config_.embed_dim;
     const int heads = config_.heads;
@@ -242,9 +354,10 @@ void VisionTransformer::attention_unfused(int batch, hipStream_t stream) {
     logits.batch.outer_stride_a = qkv_per_image;
     logits.batch.outer_stride_b = qkv_per_image;
     logits.batch.outer_stride_c = heads * logits_per_head;
-    launch_gemm(qkv_, qkv_ + embed, nullptr, attention_, logits, stream);
+    launch_gemm(stored.qkv, stored.qkv + embed, nullptr, stored.attention, logits, stream);
 
-    launch_softmax(attention_, attention_, batch * heads * token_count, token_count, stream);
+    launch_softmax(stored.attention, stored.attention, batch * heads * token_count, token_count,
+                   stream);
 
     // weights.V straight into the [tokens, heads * head_dim] context layout.
     GemmProblem context = gemm_problem(token_count, head_dim, token_count, GemmLayout::kNoTranspose);
@@ -259,11 +372,13 @@ void VisionTransformer::attention_unfused(int batch, hipStream_t stream) {
     context.batch.outer_stride_a = heads * logits_per_head;
     context.batch.outer_stride_b = qkv_per_image;
     context.batch.outer_stride_c = tokens_per_image;
-    launch_gemm(attention_, qkv_ + 2 * embed, nullptr, context_, context, stream);
+    launch_gemm(stored.attention, stored.qkv + 2 * embed, nullptr, stored.context, context, stream);
 }
 
-void VisionTransformer::run_block(const BlockWeights& block, float* tokens, int batch,
-                                  hipStream_t stream) {
+template <typename T>
+void VisionTransformer::run_block(const BlockWeights& block,
+                                  const typename Stored<T>::Matrices& matrices, Stored<T>& stored,
+                                  int batch, hipStream_t stream) {
     const int token_count = config_.token_count();
     const int embed = config_.embed_dim;
     const int heads = config_.heads;
@@ -271,37 +386,42 @@ void VisionTransformer::run_block(const BlockWeights& block, float* tokens, int 
     const int hidden = config_.mlp_hidden;
     const int rows = batch * token_count;
     const int qkv_row = 3 * embed;
+    T* const tokens = stored.tokens;
 
-    launch_layer_norm(tokens, block.norm1_gamma, block.norm1_beta, normalized_, rows, embed,
+    launch_layer_norm(tokens, block.norm1_gamma, block.norm1_beta, stored.normalized, rows, embed,
                       config_.layer_norm_epsilon, stream);
 
     // [tokens, 3, heads, head_dim] in one projection.
-    launch_gemm(normalized_, block.qkv_weight, block.qkv_bias, qkv_,
+    launch_gemm(stored.normalized, matrices.qkv, block.qkv_bias, stored.qkv,
                 gemm_problem(rows, qkv_row, embed, GemmLayout::kTransposed), stream);
 
     // softmax(Q.K^T / sqrt(head_dim)).V per (image, head) in one fused launch
-    // when the shape allows; it is bitwise equal to the three launches below.
-    if (fused_attention_) {
-        throw_on_error(cuvit_attention_f32(qkv_, context_, batch, heads, token_count, head_dim,
-                                           reinterpret_cast<cuvit_stream_t>(stream)));
+    // when the shape allows; it is bitwise equal to the three launches.
+    if constexpr (std::is_same_v<T, float>) {
+        if (fused_attention_) {
+            throw_on_error(cuvit_attention_f32(stored.qkv, stored.context, batch, heads, token_count,
+                                               head_dim, as_c(stream)));
+        } else {
+            attention_unfused(stored, batch, stream);
+        }
     } else {
-        attention_unfused(batch, stream);
+        attention_unfused(stored, batch, stream);
     }
 
     GemmProblem projection = gemm_problem(rows, embed, embed, GemmLayout::kTransposed);
     projection.epilogue.accumulate = true;
-    launch_gemm(context_, block.proj_weight, block.proj_bias, tokens, projection, stream);
+    launch_gemm(stored.context, matrices.proj, block.proj_bias, tokens, projection, stream);
 
-    launch_layer_norm(tokens, block.norm2_gamma, block.norm2_beta, normalized_, rows, embed,
+    launch_layer_norm(tokens, block.norm2_gamma, block.norm2_beta, stored.normalized, rows, embed,
                       config_.layer_norm_epsilon, stream);
 
     GemmProblem fc1 = gemm_problem(rows, hidden, embed, GemmLayout::kTransposed);
     fc1.epilogue.gelu = true;
-    launch_gemm(normalized_, block.fc1_weight, block.fc1_bias, hidden_, fc1, stream);
+    launch_gemm(stored.normalized, matrices.fc1, block.fc1_bias, stored.hidden, fc1, stream);
 
     GemmProblem fc2 = gemm_problem(rows, embed, hidden, GemmLayout::kTransposed);
     fc2.epilogue.accumulate = true;
-    launch_gemm(hidden_, block.fc2_weight, block.fc2_bias, tokens, fc2, stream);
+    launch_gemm(stored.hidden, matrices.fc2, block.fc2_bias, tokens, fc2, stream);
 }
 
 void VisionTransformer::forward(const float* images, float* logits, int batch, hipStream_t stream) {
@@ -315,13 +435,31 @@ void VisionTransformer::forward(const float* images, float* logits, int batch, h
     if (images == nullptr || logits == nullptr) {
         throw std::invalid_argument("Forward pass operands cannot be null");
     }
+    if (precision_ == Precision::kFloat32) {
+        forward_stored(f32_, images, logits, batch, stream);
+    } else {
+        forward_stored(bf16_, images, logits, batch, stream);
+    }
+}
 
+template <typename T>
+void VisionTransformer::forward_stored(Stored<T>& stored, const float* images, float* logits,
+                                       int batch, hipStream_t stream) {
+    constexpr bool kFloat = std::is_same_v<T, float>;
     const int token_count = config_.token_count();
     const int patch_count = config_.patch_count();
     const int embed = config_.embed_dim;
     const std::int64_t tokens_per_image = static_cast<std::int64_t>(token_count) * embed;
 
-    launch_extract_patches(images, patches_, batch, config_.channels, config_.image_size,
+    const T* source = nullptr;
+    if constexpr (kFloat) {
+        source = images;
+    } else {
+        throw_on_error(cuvit_convert_f32_to_bf16(
+            images, stored.images, static_cast<std::int64_t>(batch) * image_elements(), as_c(stream)));
+        source = stored.images;
+    }
+    launch_extract_patches(source, stored.patches, batch, config_.channels, config_.image_size,
                            config_.image_size, config_.patch_size, stream);
 
     // Patch embeddings land in rows 1.. of each image, with the positional
@@ -333,24 +471,29 @@ void VisionTransformer::forward(const float* images, float* logits, int batch, h
     embedding.batch.count = batch;
     embedding.batch.stride_a = static_cast<std::int64_t>(patch_count) * config_.patch_elements();
     embedding.batch.stride_c = tokens_per_image;
-    throw_on_error(capi::gemm_f32_with_addend(
-        patches_, patch_weight_, patch_bias_, position_embedding_ + embed, embed, tokens_ + embed,
-        reinterpret_cast<const cuvit_gemm_problem*>(&embedding), stream));
-    launch_broadcast(tokens_, class_position_, embed, tokens_per_image, batch, stream);
+    gemm_with_addend(stored.patches, stored.patch_weight, patch_bias_, position_embedding_ + embed,
+                     embed, stored.tokens + embed, embedding, stream);
+    launch_broadcast(stored.tokens, stored.class_position, embed, tokens_per_image, batch, stream);
 
-    for (const BlockWeights& block : blocks_) {
-        run_block(block, tokens_, batch, stream);
+    for (std::size_t index = 0; index < blocks_.size(); ++index) {
+        run_block<T>(blocks_[index], stored.blocks[index], stored, batch, stream);
     }
 
-    launch_layer_norm(tokens_, final_gamma_, final_beta_, normalized_, batch * token_count, embed,
-                      config_.layer_norm_epsilon, stream);
+    launch_layer_norm(stored.tokens, final_gamma_, final_beta_, stored.normalized,
+                      batch * token_count, embed, config_.layer_norm_epsilon, stream);
 
     // Class-token pooling: one row per image feeds the head.
     GemmProblem head = gemm_problem(1, config_.classes, embed, GemmLayout::kTransposed);
     head.batch.count = batch;
     head.batch.stride_a = tokens_per_image;
     head.batch.stride_c = config_.classes;
-    launch_gemm(normalized_, head_weight_, head_bias_, logits, head, stream);
+    if constexpr (kFloat) {
+        launch_gemm(stored.normalized, stored.head_weight, head_bias_, logits, head, stream);
+    } else {
+        launch_gemm(stored.normalized, stored.head_weight, head_bias_, stored.logits, head, stream);
+        throw_on_error(cuvit_convert_bf16_to_f32(
+            stored.logits, logits, static_cast<std::int64_t>(batch) * config_.classes, as_c(stream)));
+    }
 }
 
 std::vector<float> VisionTransformer::forward(const std::vector<float>& images) {

@@ -30,6 +30,9 @@ hipError_t extract_patches(const void* images, void* patches, int element_size, 
                            int channels, int height, int width, int patch, hipStream_t stream);
 hipError_t broadcast_f32(float* destination, const float* source, std::int64_t count,
                          std::int64_t destination_stride, int batch, hipStream_t stream);
+hipError_t broadcast_bf16(std::uint16_t* destination, const std::uint16_t* source,
+                          std::int64_t count, std::int64_t destination_stride, int batch,
+                          hipStream_t stream);
 hipError_t add_broadcast_f32(float* accumulator, const float* addend, std::int64_t count, int batch,
                              hipStream_t stream);
 
@@ -39,6 +42,10 @@ hipError_t add_f32(float* accumulator, const float* addend, std::int64_t count,
 hipError_t gelu_f32(const float* input, float* output, std::int64_t count, hipStream_t stream);
 hipError_t gelu_bf16(const std::uint16_t* input, std::uint16_t* output, std::int64_t count,
                      hipStream_t stream);
+hipError_t convert_f32_to_bf16(const float* input, std::uint16_t* output, std::int64_t count,
+                               hipStream_t stream);
+hipError_t convert_bf16_to_f32(const std::uint16_t* input, float* output, std::int64_t count,
+                               hipStream_t stream);
 
 // gemm.hip. Leading dimensions are already resolved (never zero) and the
 // batch is already flattened when it has a single outer group.

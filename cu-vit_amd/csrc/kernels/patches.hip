@@ -126,11 +126,12 @@ __global__ __launch_bounds__(kBlock) void broadcast_vector_kernel(
     }
 }
 
+template <typename Word>
 __global__ __launch_bounds__(kBlock) void broadcast_element_kernel(
-    float* __restrict__ destination, const float* __restrict__ source, std::int64_t count,
+    Word* __restrict__ destination, const Word* __restrict__ source, std::int64_t count,
     std::int64_t destination_stride, int batch) {
     for (std::int64_t slot = blockIdx.y; slot < batch; slot += gridDim.y) {
-        float* const target = destination + slot * destination_stride;
+        Word* const target = destination + slot * destination_stride;
         for (std::int64_t i = static_cast<std::int64_t>(blockIdx.x) * kBlock + threadIdx.x;
              i < count; i += static_cast<std::int64_t>(gridDim.x) * kBlock) {
             target[i] = source[i];
@@ -230,21 +231,39 @@ hipError_t extract_patches(const void* images, void* patches, int element_size, 
     return dispatch_patches<2>(images, patches, batch, channels, height, width, patch, stream);
 }
 
-hipError_t broadcast_f32(float* destination, const float* source, std::int64_t count,
-                         std::int64_t destination_stride, int batch, hipStream_t stream) {
-    if (count % 4 == 0 && destination_stride % 4 == 0 && aligned16(destination) &&
+namespace {
+
+/// The broadcast is a copy, so it is typed only by the element (Word).
+template <typename Word>
+hipError_t broadcast(Word* destination, const Word* source, std::int64_t count,
+                     std::int64_t destination_stride, int batch, hipStream_t stream) {
+    constexpr std::int64_t kVec = 16 / sizeof(Word);
+    if (count % kVec == 0 && destination_stride % kVec == 0 && aligned16(destination) &&
         aligned16(source)) {
-        const std::int64_t vectors = count / 4;
+        const std::int64_t vectors = count / kVec;
         const dim3 grid = slot_grid(vectors, batch);
         broadcast_vector_kernel<<<grid, kBlock, 0, stream>>>(
             reinterpret_cast<float4*>(destination), reinterpret_cast<const float4*>(source),
-            vectors, destination_stride / 4, batch);
+            vectors, destination_stride / kVec, batch);
     } else {
         const dim3 grid = slot_grid(count, batch);
-        broadcast_element_kernel<<<grid, kBlock, 0, stream>>>(destination, source, count,
-                                                              destination_stride, batch);
+        broadcast_element_kernel<Word><<<grid, kBlock, 0, stream>>>(destination, source, count,
+                                                                    destination_stride, batch);
     }
     return hipGetLastError();
+}
+
+} // namespace
+
+hipError_t broadcast_f32(float* destination, const float* source, std::int64_t count,
+                         std::int64_t destination_stride, int batch, hipStream_t stream) {
+    return broadcast(destination, source, count, destination_stride, batch, stream);
+}
+
+hipError_t broadcast_bf16(std::uint16_t* destination, const std::uint16_t* source,
+                          std::int64_t count, std::int64_t destination_stride, int batch,
+                          hipStream_t stream) {
+    return broadcast(destination, source, count, destination_stride, batch, stream);
 }
 
 hipError_t add_broadcast_f32(float* accumulator, const float* addend, std::int64_t count, int batch,

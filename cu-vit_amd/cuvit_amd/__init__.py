@@ -22,8 +22,9 @@ __all__ = [
     "CuvitError", "InvalidArgument", "LengthError", "HipError", "OutOfRange",
     "GemmProblem", "VitConfig", "library", "library_path", "check", "stream_handle",
     "gemm", "layer_norm", "softmax", "gelu", "extract_patches", "add", "add_broadcast",
-    "broadcast", "gemm_problem", "WeightWriter", "WeightFile", "VisionTransformer",
-    "NO_TRANSPOSE", "TRANSPOSED",
+    "broadcast", "convert_to_bf16", "convert_to_f32", "attention", "attention_supported",
+    "gemm_problem", "WeightWriter", "WeightFile", "VisionTransformer",
+    "NO_TRANSPOSE", "TRANSPOSED", "PRECISION_F32", "PRECISION_BF16",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -31,6 +32,9 @@ _DEFAULT_LIB = os.path.join(os.path.dirname(_HERE), "lib", "libcuvit_amd.so")
 
 NO_TRANSPOSE = 0
 TRANSPOSED = 1
+
+PRECISION_F32 = 0
+PRECISION_BF16 = 1
 
 OK = 0
 ERROR_INVALID_ARGUMENT = 1
@@ -155,6 +159,9 @@ _SIGNATURES = {
     "cuvit_add_f32": (_I, [_P, _P, _L, _P]),
     "cuvit_add_broadcast_f32": (_I, [_P, _P, _L, _I, _P]),
     "cuvit_broadcast_f32": (_I, [_P, _P, _L, _L, _I, _P]),
+    "cuvit_broadcast_bf16": (_I, [_P, _P, _L, _L, _I, _P]),
+    "cuvit_convert_f32_to_bf16": (_I, [_P, _P, _L, _P]),
+    "cuvit_convert_bf16_to_f32": (_I, [_P, _P, _L, _P]),
     "cuvit_attention_supported": (_I, [_I, _I]),
     "cuvit_attention_f32": (_I, [_P, _P, _I, _I, _I, _I, _P]),
     "cuvit_weight_writer_create": (_I, [ctypes.POINTER(_P)]),
@@ -171,6 +178,8 @@ _SIGNATURES = {
     "cuvit_vit_config_default": (None, [ctypes.POINTER(VitConfig)]),
     "cuvit_vit_config_validate": (_I, [ctypes.POINTER(VitConfig)]),
     "cuvit_vit_create": (_I, [ctypes.POINTER(VitConfig), _P, _I, ctypes.POINTER(_P)]),
+    "cuvit_vit_create_ex": (_I, [ctypes.POINTER(VitConfig), _P, _I, _I, ctypes.POINTER(_P)]),
+    "cuvit_vit_precision": (_I, [_P]),
     "cuvit_vit_forward": (_I, [_P, _P, _P, _I, _P]),
     "cuvit_vit_weight_bytes": (ctypes.c_uint64, [_P]),
     "cuvit_vit_activation_bytes": (ctypes.c_uint64, [_P]),
@@ -294,9 +303,21 @@ def add_broadcast(accumulator, addend, count: int, batch: int, stream=None) -> N
 
 
 def broadcast(destination, source, count: int, destination_stride: int, batch: int,
-              stream=None) -> None:
-    check(library().cuvit_broadcast_f32(_ptr(destination), _ptr(source), count,
-                                        destination_stride, batch, stream_handle(stream)))
+              stream=None, bf16: Optional[bool] = None) -> None:
+    fn = (library().cuvit_broadcast_bf16 if (bf16 if bf16 is not None else _bf16(destination))
+          else library().cuvit_broadcast_f32)
+    check(fn(_ptr(destination), _ptr(source), count, destination_stride, batch,
+             stream_handle(stream)))
+
+
+def convert_to_bf16(x, out, count: int, stream=None) -> None:
+    """fp32 -> bf16, round to nearest-even (an extension)."""
+    check(library().cuvit_convert_f32_to_bf16(_ptr(x), _ptr(out), count, stream_handle(stream)))
+
+
+def convert_to_f32(x, out, count: int, stream=None) -> None:
+    """bf16 -> fp32, exact (an extension)."""
+    check(library().cuvit_convert_bf16_to_f32(_ptr(x), _ptr(out), count, stream_handle(stream)))
 
 
 def attention_supported(tokens: int, head_dim: int) -> bool:
@@ -400,13 +421,19 @@ def validate_config(config: VitConfig) -> None:
 class VisionTransformer:
     """VisionTransformer (reference vit.hpp:53-120) over the C ABI."""
 
-    def __init__(self, config: VitConfig, weights: WeightFile, max_batch: int = 1):
+    def __init__(self, config: VitConfig, weights: WeightFile, max_batch: int = 1,
+                 precision: int = 0):
+        """precision: PRECISION_F32 (the reference's) or PRECISION_BF16 (an extension)."""
         handle = ctypes.c_void_p()
-        check(library().cuvit_vit_create(ctypes.byref(config), weights.handle, max_batch,
-                                         ctypes.byref(handle)))
+        check(library().cuvit_vit_create_ex(ctypes.byref(config), weights.handle, max_batch,
+                                            precision, ctypes.byref(handle)))
         self._handle = handle
         self.config = config
         self.max_batch = max_batch
+
+    @property
+    def precision(self) -> int:
+        return library().cuvit_vit_precision(self._handle)
 
     def forward(self, images, logits, batch: int, stream=None) -> None:
         check(library().cuvit_vit_forward(self._handle, _ptr(images), _ptr(logits), batch,

@@ -163,6 +163,16 @@ int cuvit_extract_patches_bf16(const cuvit_bf16* images, cuvit_bf16* patches, in
  * existing bf16 C is widened, added in fp32 and rounded once. */
 int cuvit_gemm_bf16(const cuvit_bf16* a, const cuvit_bf16* b, const float* bias, cuvit_bf16* c,
                     const cuvit_gemm_problem* problem, cuvit_stream_t stream);
+/* broadcast's bf16 twin: a bit copy of count values into batch slots. */
+int cuvit_broadcast_bf16(cuvit_bf16* destination, const cuvit_bf16* source, int64_t count,
+                         int64_t destination_stride, int batch, cuvit_stream_t stream);
+/* Storage conversion, no counterpart in the reference: fp32 -> bf16 rounds to
+ * nearest-even (NaN stays NaN), bf16 -> fp32 is exact. in == out is not
+ * allowed. Validation is gelu's. */
+int cuvit_convert_f32_to_bf16(const float* input, cuvit_bf16* output, int64_t count,
+                              cuvit_stream_t stream);
+int cuvit_convert_bf16_to_f32(const cuvit_bf16* input, float* output, int64_t count,
+                              cuvit_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Weight files: the reference's .cvw v1 format (weights.hpp:16-92,
@@ -218,6 +228,18 @@ int cuvit_vit_config_validate(const cuvit_vit_config* config);
 /* VisionTransformer(config, file, max_batch) (vit.cu:69-171). */
 int cuvit_vit_create(const cuvit_vit_config* config, const cuvit_weight_file* file, int max_batch,
                      cuvit_vit** model);
+/* Storage precision of a model (an extension; the reference is fp32 only). */
+typedef enum cuvit_precision {
+    CUVIT_PRECISION_F32 = 0,
+    /* bf16 GEMM weights and activations; LayerNorm gamma/beta, biases and the
+     * positional embedding stay fp32; fp32 reductions; images and logits fp32. */
+    CUVIT_PRECISION_BF16 = 1
+} cuvit_precision;
+/* cuvit_vit_create with a storage precision (a cuvit_precision value). */
+int cuvit_vit_create_ex(const cuvit_vit_config* config, const cuvit_weight_file* file,
+                        int max_batch, int precision, cuvit_vit** model);
+/* The model's cuvit_precision, or -1 for a null model. */
+int cuvit_vit_precision(const cuvit_vit* model);
 /* VisionTransformer::forward(images, logits, batch, stream) (vit.cu:263-317). */
 int cuvit_vit_forward(cuvit_vit* model, const float* images, float* logits, int batch,
                       cuvit_stream_t stream);

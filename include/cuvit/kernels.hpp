@@ -118,6 +118,8 @@ void launch_softmax(const std::uint16_t* input, std::uint16_t* output, int rows,
 void launch_extract_patches(const std::uint16_t* images, std::uint16_t* patches, int batch,
                             int channels, int height, int width, int patch,
                             hipStream_t stream = nullptr);
+void launch_broadcast(std::uint16_t* destination, const std::uint16_t* source, std::int64_t count,
+                      std::int64_t destination_stride, int batch, hipStream_t stream = nullptr);
 
 /// Throws the exception matching a C-ABI status (no-op on CUVIT_OK).
 void throw_on_error(int status);

@@ -4,7 +4,7 @@
 // (VitConfig 15-35, BlockWeights 38-51, VisionTransformer 53-120) and
 // src/model/vit.cu. It sequences the layer kernels of cuvit/kernels.hpp over
 // activations carved once from a DeviceArena, so a forward pass allocates
-// nothing and issues 12 * 9 + 6 launches on one stream.
+// nothing and queues every launch on one stream.
 
 #include "cuvit/device_arena.hpp"
 #include "cuvit/device_buffer.hpp"
@@ -14,10 +14,19 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <cstdint>
 #include <string>
 #include <vector>
 
 namespace cuvit {
+
+/// Storage precision of a model. kBFloat16 is an extension (the reference is
+/// fp32 only, README.md:472-473): the GEMM weight matrices and every
+/// activation are bf16, while LayerNorm's gamma and beta, the biases and the
+/// positional embedding stay fp32, every reduction and epilogue runs in fp32,
+/// and each stored value is rounded once, to nearest-even. Images in and
+/// logits out stay fp32 either way.
+enum class Precision { kFloat32, kBFloat16 };
 
 /// Shape of a Vision Transformer; the defaults are ViT-Tiny/16 at 224x224.
 struct VitConfig {
@@ -60,8 +69,10 @@ struct BlockWeights {
 class VisionTransformer final {
   public:
     /// Uploads @p file (shape-checked against @p config, timm names) and
-    /// reserves activations for @p max_batch images.
-    VisionTransformer(const VitConfig& config, const WeightFile& file, int max_batch = 1);
+    /// reserves activations for @p max_batch images. With kBFloat16 the GEMM
+    /// weights are rounded to bf16 as they are staged.
+    VisionTransformer(const VitConfig& config, const WeightFile& file, int max_batch = 1,
+                      Precision precision = Precision::kFloat32);
 
     /// @p batch planar images in device memory -> batch x classes logits in
     /// device memory, queued on @p stream.
@@ -72,6 +83,7 @@ class VisionTransformer final {
 
     [[nodiscard]] const VitConfig& config() const noexcept { return config_; }
     [[nodiscard]] int max_batch() const noexcept { return max_batch_; }
+    [[nodiscard]] Precision precision() const noexcept { return precision_; }
     [[nodiscard]] std::size_t image_elements() const noexcept;
     [[nodiscard]] std::size_t weight_bytes() const noexcept { return weights_.used(); }
     [[nodiscard]] std::size_t activation_bytes() const noexcept { return activations_.used(); }
@@ -80,13 +92,46 @@ class VisionTransformer final {
     [[nodiscard]] static std::vector<std::string> expected_tensor_names(const VitConfig& config);
 
   private:
-    void run_block(const BlockWeights& block, float* tokens, int batch, hipStream_t stream);
+    /// What depends on the storage type T (float or bf16 bits): the GEMM
+    /// weight matrices, the class row cls + pos[0] and the activations.
+    template <typename T> struct Stored {
+        struct Matrices {
+            const T* qkv = nullptr;
+            const T* proj = nullptr;
+            const T* fc1 = nullptr;
+            const T* fc2 = nullptr;
+        };
+        const T* patch_weight = nullptr;
+        const T* head_weight = nullptr;
+        const T* class_position = nullptr; // cls + pos[0]
+        std::vector<Matrices> blocks;
+
+        T* images = nullptr; // the input in storage precision (bf16 only)
+        T* patches = nullptr;
+        T* tokens = nullptr;
+        T* normalized = nullptr;
+        T* qkv = nullptr;
+        T* attention = nullptr;
+        T* context = nullptr;
+        T* hidden = nullptr;
+        T* logits = nullptr; // the head's output before widening (bf16 only)
+    };
+
+    template <typename T> void load(const WeightFile& file, Stored<T>& stored);
+    template <typename T> void reserve_activations(Stored<T>& stored);
+    template <typename T>
+    void forward_stored(Stored<T>& stored, const float* images, float* logits, int batch,
+                        hipStream_t stream);
+    template <typename T>
+    void run_block(const BlockWeights& block, const typename Stored<T>::Matrices& matrices,
+                   Stored<T>& stored, int batch, hipStream_t stream);
     /// The reference's three attention launches (vit.cu:205-245), used when
-    /// the fused kernel does not cover the shape.
-    void attention_unfused(int batch, hipStream_t stream);
+    /// the fused kernel does not cover the shape or the precision.
+    template <typename T> void attention_unfused(Stored<T>& stored, int batch, hipStream_t stream);
 
     VitConfig config_;
     int max_batch_ = 1;
+    Precision precision_ = Precision::kFloat32;
     bool fused_attention_ = false;
 
     DeviceArena weights_;
@@ -94,22 +139,18 @@ class VisionTransformer final {
 
     const float* class_token_ = nullptr;
     const float* position_embedding_ = nullptr;
-    const float* class_position_ = nullptr; // cls + pos[0]
-    const float* patch_weight_ = nullptr;
+    const float* patch_weight_ = nullptr; // fp32 models only
     const float* patch_bias_ = nullptr;
     const float* final_gamma_ = nullptr;
     const float* final_beta_ = nullptr;
-    const float* head_weight_ = nullptr;
+    const float* head_weight_ = nullptr; // fp32 models only
     const float* head_bias_ = nullptr;
+    /// fp32 parameters of each block; the GEMM matrices are set for fp32
+    /// models only (bf16 models keep theirs in bf16_.blocks).
     std::vector<BlockWeights> blocks_;
 
-    float* patches_ = nullptr;
-    float* tokens_ = nullptr;
-    float* normalized_ = nullptr;
-    float* qkv_ = nullptr;
-    float* attention_ = nullptr;
-    float* context_ = nullptr;
-    float* hidden_ = nullptr;
+    Stored<float> f32_;
+    Stored<std::uint16_t> bf16_;
 };
 
 } // namespace cuvit

@@ -14,6 +14,10 @@
 //   add, add_broadcast, broadcast - closed forms.
 //   vit_forward - assembled from the pinned pieces; cross-checked against a
 //     numpy restatement of tests/reference/vit.hpp at a small configuration.
+//   vit_forward_bf16 - the same code with rounding inserted (no reference: the
+//     bf16 model is an extension); pinned by reducing to vit_forward on
+//     bf16-exact data with rounding as the only difference, by its rounding
+//     agreeing with round_bf16, and by staying within bf16 error of vit_forward.
 //   generator - the mt19937_64 10000th-output value fixed by the C++ standard,
 //     committed first-values fixtures, distribution moments.
 //   round_bf16 - exhaustive properties on special values and ties.
@@ -29,6 +33,22 @@
 #include <vector>
 
 namespace {
+
+/// @p value rounded to the nearest bf16 (ties to even), widened back to float;
+/// a NaN stays NaN. The same rounding as oracle_round_bf16.
+float round_to_bf16_value(float value) {
+    std::uint32_t bits = 0;
+    std::memcpy(&bits, &value, sizeof(bits));
+    if ((bits & 0x7F800000U) == 0x7F800000U && (bits & 0x007FFFFFU) != 0) {
+        bits |= 0x00400000U;
+    } else {
+        bits += 0x7FFFU + ((bits >> 16) & 1U);
+    }
+    bits &= 0xFFFF0000U;
+    float out = 0.0F;
+    std::memcpy(&out, &bits, sizeof(out));
+    return out;
+}
 
 float gelu_value(float value) {
     // tests/reference/linear_algebra.hpp:120-123 (erf form).
@@ -245,8 +265,18 @@ void oracle_broadcast(float* destination, const float* source, int64_t count,
 
 // tests/reference/vit.hpp:57-112 (forward) and 134-206 (run_block): one image,
 // one named buffer per step, per-head attention in plain loops.
-void oracle_vit_forward(const oracle_vit_config* cfg, const float* const* tensors,
-                        const float* image, float* logits) {
+//
+// With reduced set, the same steps with every stored value rounded to bf16 at
+// the point where the bf16 model stores it (the extension has no reference;
+// this is its definition): the image, the GEMM weight matrices, every token
+// row after the embedding and after each residual accumulate, each LayerNorm
+// output, q/k/v, the attention logits (after the 1/sqrt(head_dim) scale), the
+// attention weights, the context, the MLP hidden (after GELU) and the logits.
+// Biases, gamma, beta, cls and pos stay fp32; an accumulate rounds
+// x + (sum + bias) once. With reduced clear nothing is rounded and this is
+// the fp32 forward above.
+static void vit_forward(const oracle_vit_config* cfg, const float* const* tensors,
+                        const float* image_in, float* logits, bool reduced) {
     const int embed = cfg->embed_dim;
     const int across = cfg->image_size / cfg->patch_size;
     const int patch_count = across * across;
@@ -257,24 +287,43 @@ void oracle_vit_forward(const oracle_vit_config* cfg, const float* const* tensor
     const int hidden = cfg->mlp_hidden;
     const float eps = cfg->layer_norm_epsilon;
 
+    auto round = [reduced](std::vector<float>& v) {
+        if (reduced) {
+            for (float& x : v) {
+                x = round_to_bf16_value(x);
+            }
+        }
+    };
+    // A GEMM weight matrix as the model stores it.
+    auto matrix = [&](const float* w, std::size_t count) {
+        std::vector<float> m(w, w + count);
+        round(m);
+        return m;
+    };
+
     const float* cls = tensors[0];
     const float* pos = tensors[1];
-    const float* patch_weight = tensors[2];
+    const std::vector<float> patch_weight =
+        matrix(tensors[2], static_cast<std::size_t>(embed) * patch_elements);
     const float* patch_bias = tensors[3];
 
+    std::vector<float> image(image_in, image_in + static_cast<std::size_t>(cfg->channels) *
+                                                      cfg->image_size * cfg->image_size);
+    round(image);
     std::vector<float> patches(static_cast<std::size_t>(patch_count) * patch_elements);
-    oracle_extract_patches(image, patches.data(), 1, cfg->channels, cfg->image_size,
+    oracle_extract_patches(image.data(), patches.data(), 1, cfg->channels, cfg->image_size,
                            cfg->image_size, cfg->patch_size);
 
     std::vector<float> x(static_cast<std::size_t>(tokens) * embed);
     for (int i = 0; i < embed; ++i) {
         x[static_cast<std::size_t>(i)] = cls[i];
     }
-    oracle_gemm_transposed(patches.data(), patch_weight, patch_bias, x.data() + embed, patch_count,
-                           embed, patch_elements, 1.0F);
+    oracle_gemm_transposed(patches.data(), patch_weight.data(), patch_bias, x.data() + embed,
+                           patch_count, embed, patch_elements, 1.0F);
     for (std::size_t i = 0; i < x.size(); ++i) {
         x[i] += pos[i];
     }
+    round(x);
 
     std::vector<float> normalized(x.size());
     std::vector<float> qkv(static_cast<std::size_t>(tokens) * 3 * embed);
@@ -289,8 +338,16 @@ void oracle_vit_forward(const oracle_vit_config* cfg, const float* const* tensor
     for (int block = 0; block < cfg->depth; ++block) {
         const float* const* t = tensors + 4 + 12 * block;
         // t: norm1 w/b, qkv w/b, proj w/b, norm2 w/b, fc1 w/b, fc2 w/b
+        const std::vector<float> qkv_weight = matrix(t[2], static_cast<std::size_t>(row) * embed);
+        const std::vector<float> proj_weight = matrix(t[4], static_cast<std::size_t>(embed) * embed);
+        const std::vector<float> fc1_weight = matrix(t[8], static_cast<std::size_t>(hidden) * embed);
+        const std::vector<float> fc2_weight = matrix(t[10], static_cast<std::size_t>(embed) * hidden);
+
         oracle_layer_norm(x.data(), t[0], t[1], normalized.data(), tokens, embed, eps);
-        oracle_gemm_transposed(normalized.data(), t[2], t[3], qkv.data(), tokens, row, embed, 1.0F);
+        round(normalized);
+        oracle_gemm_transposed(normalized.data(), qkv_weight.data(), t[3], qkv.data(), tokens, row,
+                               embed, 1.0F);
+        round(qkv);
         for (int h = 0; h < heads; ++h) {
             for (int q = 0; q < tokens; ++q) {
                 for (int kk = 0; kk < tokens; ++kk) {
@@ -302,7 +359,9 @@ void oracle_vit_forward(const oracle_vit_config* cfg, const float* const* tensor
                     logits_tt[static_cast<std::size_t>(q) * tokens + kk] = sum * scale;
                 }
             }
+            round(logits_tt);
             oracle_softmax(logits_tt.data(), weights_tt.data(), tokens, tokens);
+            round(weights_tt);
             for (int q = 0; q < tokens; ++q) {
                 for (int d = 0; d < head_dim; ++d) {
                     float sum = 0.0F;
@@ -314,22 +373,47 @@ void oracle_vit_forward(const oracle_vit_config* cfg, const float* const* tensor
                 }
             }
         }
-        oracle_gemm_transposed(context.data(), t[4], t[5], projected.data(), tokens, embed, embed, 1.0F);
+        round(context);
+        oracle_gemm_transposed(context.data(), proj_weight.data(), t[5], projected.data(), tokens,
+                               embed, embed, 1.0F);
         for (std::size_t i = 0; i < x.size(); ++i) {
             x[i] += projected[i];
         }
+        round(x);
         oracle_layer_norm(x.data(), t[6], t[7], normalized.data(), tokens, embed, eps);
-        oracle_gemm_transposed(normalized.data(), t[8], t[9], mlp.data(), tokens, hidden, embed, 1.0F);
+        round(normalized);
+        oracle_gemm_transposed(normalized.data(), fc1_weight.data(), t[9], mlp.data(), tokens,
+                               hidden, embed, 1.0F);
         oracle_gelu(mlp.data(), mlp.data(), static_cast<int64_t>(mlp.size()));
-        oracle_gemm_transposed(mlp.data(), t[10], t[11], projected.data(), tokens, embed, hidden, 1.0F);
+        round(mlp);
+        oracle_gemm_transposed(mlp.data(), fc2_weight.data(), t[11], projected.data(), tokens, embed,
+                               hidden, 1.0F);
         for (std::size_t i = 0; i < x.size(); ++i) {
             x[i] += projected[i];
         }
+        round(x);
     }
 
     const float* const* tail = tensors + 4 + 12 * cfg->depth;
+    const std::vector<float> head_weight =
+        matrix(tail[2], static_cast<std::size_t>(cfg->classes) * embed);
     oracle_layer_norm(x.data(), tail[0], tail[1], normalized.data(), tokens, embed, eps);
-    oracle_gemm_transposed(normalized.data(), tail[2], tail[3], logits, 1, cfg->classes, embed, 1.0F);
+    round(normalized);
+    std::vector<float> out(static_cast<std::size_t>(cfg->classes));
+    oracle_gemm_transposed(normalized.data(), head_weight.data(), tail[3], out.data(), 1,
+                           cfg->classes, embed, 1.0F);
+    round(out);
+    std::copy(out.begin(), out.end(), logits);
+}
+
+void oracle_vit_forward(const oracle_vit_config* cfg, const float* const* tensors,
+                        const float* image, float* logits) {
+    vit_forward(cfg, tensors, image, logits, false);
+}
+
+void oracle_vit_forward_bf16(const oracle_vit_config* cfg, const float* const* tensors,
+                             const float* image, float* logits) {
+    vit_forward(cfg, tensors, image, logits, true);
 }
 
 void oracle_round_bf16(const float* input, uint16_t* output, int64_t count) {

@@ -64,6 +64,11 @@ void oracle_broadcast(float* destination, const float* source, int64_t count,
  * VisionTransformer::expected_tensor_names. */
 void oracle_vit_forward(const oracle_vit_config* config, const float* const* tensors,
                         const float* image, float* logits);
+/* The bf16 model's forward (an extension): oracle_vit_forward with every
+ * stored activation and each GEMM weight matrix rounded to bf16 where the
+ * model stores it; logits are the rounded values widened to float. */
+void oracle_vit_forward_bf16(const oracle_vit_config* config, const float* const* tensors,
+                             const float* image, float* logits);
 /* Round to bfloat16 bits, nearest-even (NaN kept quiet). */
 void oracle_round_bf16(const float* input, uint16_t* output, int64_t count);
 

@@ -136,6 +136,7 @@ class Oracle(_Linear):
             "oracle_add_broadcast": (None, [_P, _P, _L, _I]),
             "oracle_broadcast": (None, [_P, _P, _L, _L, _I]),
             "oracle_vit_forward": (None, [ctypes.POINTER(OracleVitConfig), ctypes.POINTER(_P), _P, _P]),
+            "oracle_vit_forward_bf16": (None, [ctypes.POINTER(OracleVitConfig), ctypes.POINTER(_P), _P, _P]),
             "oracle_round_bf16": (None, [_P, _P, _L]),
             "oracle_generator_create": (_P, [ctypes.c_uint64]),
             "oracle_generator_uniform": (None, [_P, _P, _L, _F, _F]),
@@ -188,7 +189,9 @@ class Oracle(_Linear):
         self.lib.oracle_broadcast(_p(destination), _p(source), count, stride, batch)
         return destination
 
-    def vit_forward(self, config, tensors: Sequence[np.ndarray], image) -> np.ndarray:
+    def vit_forward(self, config, tensors: Sequence[np.ndarray], image,
+                    bf16: bool = False) -> np.ndarray:
+        """One image's logits; bf16 selects the bf16 model's rounding points."""
         cfg = OracleVitConfig(config.image_size, config.patch_size, config.channels,
                               config.embed_dim, config.depth, config.heads, config.mlp_hidden,
                               config.classes, config.layer_norm_epsilon)
@@ -196,7 +199,8 @@ class Oracle(_Linear):
         pointers = (_P * len(arrays))(*[a.ctypes.data for a in arrays])
         image = _f32(image)
         logits = np.empty(config.classes, dtype=np.float32)
-        self.lib.oracle_vit_forward(ctypes.byref(cfg), pointers, _p(image), _p(logits))
+        fn = self.lib.oracle_vit_forward_bf16 if bf16 else self.lib.oracle_vit_forward
+        fn(ctypes.byref(cfg), pointers, _p(image), _p(logits))
         return logits
 
     def round_bf16(self, x) -> np.ndarray:

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import bf16_bits, bf16_tensor, to_device
+from conftest import bf16_bits, bf16_tensor, to_device, to_host
 from numerics import TestFailure, require_close, require_exact
 from oracle import bf16_to_float
 
@@ -198,3 +198,121 @@ def test_gemm_bf16_batched_tile_blocks(cuvit, oracle, device):
         expected = oracle.gemm_transposed(ae, be, None, m, n, k)
         scale = oracle.term_magnitudes(ae, be, m, n, k, True)
         require_gemm_close(actual[e], expected, scale, f"bf16 batched entry {e}")
+
+
+# -- storage conversion and the bf16 broadcast (extensions) ----------------------
+
+SPECIALS = np.array([0.0, -0.0, 1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -(1.0 + 2 ** -8), 3.0e38,
+                     np.finfo(np.float32).max, np.inf, -np.inf, np.nan, 1e-40, -1e-45,
+                     np.finfo(np.float32).tiny], np.float32)
+
+
+@pytest.mark.parametrize("count,offset", [(1 << 20, 0), (4099, 0), (4099, 3), (7, 1), (1, 0)])
+def test_convert_to_bf16_rounds_like_the_oracle(cuvit, oracle, device, count, offset):
+    """Nearest-even rounding, bit-exact against the oracle's round_bf16 (pinned
+    to torch's float32 -> bfloat16), ties and specials included; offsets
+    exercise the unaligned scalar path and the vector tail."""
+    values = oracle.generator(900 + count).normal(count, 0.0, 50.0)
+    values[:min(count, SPECIALS.size)] = SPECIALS[:min(count, SPECIALS.size)]
+    x = to_device(np.concatenate([np.zeros(offset, np.float32), values]), device)[offset:]
+    y = torch.empty(count + 1, dtype=torch.bfloat16, device=device)[1:] if offset else \
+        torch.empty(count, dtype=torch.bfloat16, device=device)
+    cuvit.convert_to_bf16(x, y, count)
+    actual, expected = bf16_bits(y), oracle.round_bf16(values)
+    nan = np.isnan(values)
+    require_exact(actual[~nan], expected[~nan], f"fp32 -> bf16 conversion, {count} at +{offset}")
+    if nan.any():
+        assert np.all((actual[nan] & 0x7F80) == 0x7F80) and np.all((actual[nan] & 0x7F) != 0)
+
+
+@pytest.mark.parametrize("count,offset", [(1 << 20, 0), (4099, 0), (4099, 5), (3, 1)])
+def test_convert_to_f32_is_exact(cuvit, oracle, device, count, offset):
+    bits = oracle.generator(910 + count).integers(count + offset, 0, 1 << 16).astype(np.uint16)
+    bits[offset] = 0x7FC1  # a NaN payload survives widening
+    x = bf16_tensor(bits, device)[offset:]
+    y = torch.empty(count, device=device)
+    cuvit.convert_to_f32(x, y, count)
+    actual = to_host(y).view(np.uint32)
+    require_exact(actual, bits[offset:].astype(np.uint32) << 16, "bf16 -> fp32 widening")
+
+
+@pytest.mark.parametrize("count,stride,batch", [(768, 197 * 768, 64), (192, 197 * 192, 32),
+                                                (24, 17 * 24, 5), (7, 11, 3), (768, 768, 1)])
+def test_broadcast_bf16_bit_exact(cuvit, oracle, device, count, stride, batch):
+    """broadcast (normalization.cu:194-201) moving bf16 bits; whatever lies
+    between the slots is left alone."""
+    source = oracle.generator(920 + count).integers(count, 0, 1 << 16).astype(np.uint16)
+    destination = oracle.generator(921).integers(stride * batch, 0, 1 << 16).astype(np.uint16)
+    expected = destination.copy().reshape(batch, stride)
+    expected[:, :count] = source
+    d = bf16_tensor(destination, device)
+    cuvit.broadcast(d, bf16_tensor(source, device), count, stride, batch)
+    require_exact(bf16_bits(d), expected.reshape(-1), "bf16 broadcast")
+
+
+# -- rounding-boundary parity ----------------------------------------------------
+
+def ulp_distance(a_bits, b_bits) -> np.ndarray:
+    """Distance in bf16 ulps between two arrays of bf16 bit patterns."""
+    def ordered(bits):
+        bits = bits.astype(np.int32)
+        return np.where(bits & 0x8000, -(bits & 0x7FFF), bits & 0x7FFF)
+    return np.abs(ordered(a_bits) - ordered(b_bits))
+
+
+def require_rounded(oracle, actual_bits, expected, context, max_fraction=1.0e-3, max_ulp=None):
+    """The GPU's bf16 bits equal the oracle's fp32 result rounded to bf16,
+    except where the two fp32 values straddle a rounding boundary because the
+    sums ran in a different order: at most @p max_fraction of the values (one
+    flip each is ~1e-5 to 2e-4 of the values in practice)."""
+    distance = ulp_distance(actual_bits.reshape(-1), oracle.round_bf16(expected.reshape(-1)))
+    fraction = np.count_nonzero(distance) / distance.size
+    if fraction > max_fraction:
+        raise TestFailure(f"{context}: {fraction:.2e} of the values differ from the rounded oracle")
+    if max_ulp is not None and distance.max() > max_ulp:
+        raise TestFailure(f"{context}: a value is {distance.max()} ulps from the rounded oracle")
+
+
+@pytest.mark.parametrize("rows,columns", [(6304, 192), (394, 768)])
+def test_layer_norm_bf16_rounds_like_the_oracle(cuvit, oracle, device, rows, columns):
+    bits, values = bf16_inputs(oracle, 940 + columns, rows * columns)
+    g = oracle.generator(941)
+    gamma, beta = g.normal(columns, 1.0, 0.02), g.normal(columns, 0.0, 0.02)
+    y = torch.empty(rows * columns, dtype=torch.bfloat16, device=device)
+    cuvit.layer_norm(bf16_tensor(bits, device), to_device(gamma, device), to_device(beta, device),
+                     y, rows, columns, 1e-6)
+    expected = oracle.layer_norm(values.reshape(rows, columns), gamma, beta, 1e-6)
+    # no ulp bound: where beta cancels the normalized term, the result is near
+    # zero and one fp32 ulp of the inputs is several bf16 ulps of it
+    require_rounded(oracle, bf16_bits(y), expected, "bf16 layer norm")
+
+
+@pytest.mark.parametrize("stddev", [0.3, 3.0])
+def test_softmax_bf16_rounds_like_the_oracle(cuvit, oracle, device, stddev):
+    rows = 32 * 3 * 197
+    bits, values = bf16_inputs(oracle, 950, rows * 197, 0.0, stddev)
+    x = bf16_tensor(bits, device)
+    cuvit.softmax(x, x, rows, 197)
+    require_rounded(oracle, bf16_bits(x), oracle.softmax(values.reshape(rows, 197)),
+                    "bf16 softmax in place", max_ulp=1)
+
+
+@pytest.mark.parametrize("m,n,k,gelu,accumulate", [(6304, 576, 192, 0, 0), (6304, 768, 192, 1, 0),
+                                                   (6304, 192, 768, 0, 1), (394, 192, 192, 0, 1),
+                                                   (392, 192, 768, 0, 0)])
+def test_gemm_bf16_rounds_like_the_oracle(cuvit, oracle, device, m, n, k, gelu, accumulate):
+    """The model's GEMM shapes at ViT-Tiny: QKV, FC1 + GELU, FC2 and the
+    projection accumulating into the residual stream, the embedding."""
+    a_bits, a = bf16_inputs(oracle, 960 + n, m * k)
+    b_bits, b = bf16_inputs(oracle, 961 + k, n * k, 0.0, 0.02)
+    c_bits, c = bf16_inputs(oracle, 962, m * n)
+    bias = oracle.generator(963).normal(n, 0.0, 0.02)
+    out = bf16_tensor(c_bits, device)
+    p = cuvit.gemm_problem(m, n, k, cuvit.TRANSPOSED)
+    p.epilogue.gelu, p.epilogue.accumulate = gelu, accumulate
+    cuvit.gemm(bf16_tensor(a_bits, device), bf16_tensor(b_bits, device), to_device(bias, device),
+               out, p)
+    expected = c.copy()
+    oracle.gemm_problem_run(a, b, bias, expected, m=m, n=n, k=k, layout=1, accumulate=accumulate,
+                            gelu=gelu)
+    require_rounded(oracle, bf16_bits(out), expected, f"bf16 GEMM {m}x{n}x{k}")

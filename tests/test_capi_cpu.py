@@ -56,6 +56,9 @@ def test_zero_extents_return_before_any_check(lib):
     assert lib.cuvit_softmax_bf16(None, None, 4, 0, None) == 0
     assert lib.cuvit_attention_f32(None, None, 0, 3, 197, 64, None) == 0
     assert lib.cuvit_attention_f32(None, None, 2, 3, 0, 64, None) == 0
+    assert lib.cuvit_broadcast_bf16(None, None, 0, 0, 3, None) == 0
+    assert lib.cuvit_convert_f32_to_bf16(None, None, 0, None) == 0
+    assert lib.cuvit_convert_bf16_to_f32(None, None, 0, None) == 0
 
 
 @pytest.mark.parametrize("call,message", [
@@ -97,6 +100,11 @@ def test_zero_extents_return_before_any_check(lib):
      "Fused attention supports head_dim 64 and at most 256 tokens"),
     (lambda l: l.cuvit_attention_f32(FAKE + 4, FAKE, 2, 3, 197, 64, None),
      "Fused attention needs 16-byte aligned operands"),
+    (lambda l: l.cuvit_broadcast_bf16(FAKE, FAKE, 8, 4, 2, None), "Broadcast extents are inconsistent"),
+    (lambda l: l.cuvit_broadcast_bf16(None, FAKE, 4, 8, 2, None), "Broadcast operands cannot be null"),
+    (lambda l: l.cuvit_convert_f32_to_bf16(FAKE, FAKE, -1, None), "GELU element count cannot be negative"),
+    (lambda l: l.cuvit_convert_f32_to_bf16(FAKE, None, 4, None), "GELU operands cannot be null"),
+    (lambda l: l.cuvit_convert_bf16_to_f32(None, FAKE, 4, None), "GELU operands cannot be null"),
 ])
 def test_invalid_arguments(cuvit, lib, call, message):
     status = call(lib)
@@ -111,6 +119,8 @@ def test_oversized_launches_are_length_errors(cuvit, lib):
                    lib.cuvit_add_f32(FAKE, FAKE, huge, None),
                    lib.cuvit_add_broadcast_f32(FAKE, FAKE, 1 << 30, 1 << 20, None),
                    lib.cuvit_broadcast_f32(FAKE, FAKE, 1 << 30, 1 << 30, 1 << 20, None),
+                   lib.cuvit_broadcast_bf16(FAKE, FAKE, 1 << 30, 1 << 30, 1 << 20, None),
+                   lib.cuvit_convert_f32_to_bf16(FAKE, FAKE, huge, None),
                    lib.cuvit_extract_patches_f32(FAKE, FAKE, 1 << 20, 3, 1 << 14, 1 << 14, 16, None)):
         assert status == cuvit.ERROR_LENGTH
         assert "grid limit" in lib.cuvit_last_error().decode()
@@ -198,3 +208,20 @@ def test_expected_tensor_names(cuvit):
     assert len(names) == 152
     assert names[0][0] == "cls_token" and names[-1][0] == "head.bias"
     assert sum(int(__import__("numpy").prod(s)) for _, s in names) == 5717416
+
+
+def test_model_precision_is_validated_before_any_allocation(cuvit, lib, tmp_path):
+    """cuvit_vit_create_ex rejects an unknown precision before it touches the device."""
+    writer = cuvit.WeightWriter()
+    writer.add("cls_token", __import__("numpy").zeros((1, 1, 4), "float32"))
+    path = str(tmp_path / "one.cvw")
+    writer.write(path)
+    weights = cuvit.WeightFile(path)
+    config = cuvit.default_config()
+    handle = ctypes.c_void_p()
+    status = lib.cuvit_vit_create_ex(ctypes.byref(config), weights.handle, 1, 7, ctypes.byref(handle))
+    assert status == cuvit.ERROR_INVALID_ARGUMENT
+    assert lib.cuvit_last_error().decode() == "precision is not a cuvit_precision value"
+    assert not handle.value
+    assert lib.cuvit_vit_precision(None) == -1
+    assert (cuvit.PRECISION_F32, cuvit.PRECISION_BF16) == (0, 1)

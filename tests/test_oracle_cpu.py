@@ -20,6 +20,7 @@ import numpy as np
 import pytest
 
 from numerics import compare_close, compare_close_scaled, require_close, require_close_scaled, require_exact
+from oracle import bf16_to_float
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -211,37 +212,49 @@ def test_broadcasts_closed_form(oracle):
                   "add_broadcast")
 
 
-def numpy_vit(config, tensors, image):
-    """tests/reference/vit.hpp:57-206 written with numpy array operations (float64)."""
+def to_bf16(a):
+    """Nearest bf16 (ties to even) of float64 values, through torch's float32 -> bfloat16."""
+    import torch
+
+    return torch.from_numpy(np.asarray(a, np.float32)).to(torch.bfloat16).to(torch.float64).numpy()
+
+
+def numpy_vit(config, tensors, image, bf16=False):
+    """tests/reference/vit.hpp:57-206 written with numpy array operations (float64).
+
+    bf16 rounds what the bf16 model stores, as a separate statement of those
+    points: the image and GEMM weights, then each stored activation."""
+    r = to_bf16 if bf16 else (lambda a: a)
     t = [np.asarray(v, np.float64) for v in tensors]
     e, p, c, s = config.embed_dim, config.patch_size, config.channels, config.image_size
     n = s // p
     heads, hd = config.heads, config.embed_dim // config.heads
-    img = np.asarray(image, np.float64).reshape(c, n, p, n, p).transpose(1, 3, 0, 2, 4)
+    img = r(np.asarray(image, np.float64)).reshape(c, n, p, n, p).transpose(1, 3, 0, 2, 4)
     patches = img.reshape(n * n, c * p * p)
-    x = np.concatenate([t[0].reshape(1, e), patches @ t[2].reshape(e, -1).T + t[3]]) + t[1].reshape(-1, e)
+    x = r(np.concatenate([t[0].reshape(1, e), patches @ r(t[2].reshape(e, -1)).T + t[3]])
+          + t[1].reshape(-1, e))
 
     def ln(v, g, b):
         mu = v.mean(1, keepdims=True)
-        return (v - mu) / np.sqrt(v.var(1, keepdims=True) + config.layer_norm_epsilon) * g + b
+        return r((v - mu) / np.sqrt(v.var(1, keepdims=True) + config.layer_norm_epsilon) * g + b)
 
     for blk in range(config.depth):
         w = t[4 + 12 * blk: 16 + 12 * blk]
         h = ln(x, w[0], w[1])
-        qkv = (h @ w[2].T + w[3]).reshape(-1, 3, heads, hd)
+        qkv = r(h @ r(w[2]).T + w[3]).reshape(-1, 3, heads, hd)
         q, k, v = qkv[:, 0].transpose(1, 0, 2), qkv[:, 1].transpose(1, 0, 2), qkv[:, 2].transpose(1, 0, 2)
-        logits = q @ k.transpose(0, 2, 1) / math.sqrt(hd)
+        logits = r(q @ k.transpose(0, 2, 1) / math.sqrt(hd))
         att = np.exp(logits - logits.max(-1, keepdims=True))
-        att /= att.sum(-1, keepdims=True)
-        ctx = (att @ v).transpose(1, 0, 2).reshape(-1, e)
-        x = x + ctx @ w[4].T + w[5]
+        att = r(att / att.sum(-1, keepdims=True))
+        ctx = r((att @ v).transpose(1, 0, 2).reshape(-1, e))
+        x = r(x + (ctx @ r(w[4]).T + w[5]))
         h = ln(x, w[6], w[7])
-        z = h @ w[8].T + w[9]
-        z = 0.5 * z * (1 + np.vectorize(math.erf)(z / math.sqrt(2)))
-        x = x + z @ w[10].T + w[11]
+        z = h @ r(w[8]).T + w[9]
+        z = r(0.5 * z * (1 + np.vectorize(math.erf)(z / math.sqrt(2))))
+        x = r(x + (z @ r(w[10]).T + w[11]))
     tail = t[4 + 12 * config.depth:]
     cls = ln(x[:1], tail[0], tail[1])
-    return (cls @ tail[2].T + tail[3])[0]
+    return r(cls @ r(tail[2]).T + tail[3])[0]
 
 
 def test_vit_forward_against_numpy(cuvit, oracle):
@@ -253,6 +266,33 @@ def test_vit_forward_against_numpy(cuvit, oracle):
         image = random_image(oracle, config, seed)
         require_close(oracle.vit_forward(config, tensors, image), numpy_vit(config, tensors, image),
                       "oracle ViT vs numpy ViT", 1e-4, 1e-4)
+
+
+def relative_l2(a, b) -> float:
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+def test_vit_forward_bf16_against_numpy(cuvit, oracle):
+    """The bf16 model's oracle (float32 loops, rounding where the model stores)
+    against numpy_vit's own statement of the rounding points (float64 array
+    operations). They agree to 1e-3 relative (measured: 0, every logit equal);
+    leaving out any one rounding point (the attention weights, the context,
+    the logits, q/k/v or the MLP hidden) moves the numpy logits by 3.7e-3 to
+    8.9e-3 relative at these seeds, so a dropped or misplaced rounding fails.
+    Against the fp32 oracle the gap is bf16-sized (7e-3 to 1.5e-2)."""
+    from vit_support import random_image, random_weights, small_config
+
+    config = small_config(cuvit)
+    tensors = [v for _, v in random_weights(cuvit, oracle, config, 1234)]
+    for seed in (1, 2, 3):
+        image = random_image(oracle, config, seed)
+        reduced = oracle.vit_forward(config, tensors, image, bf16=True)
+        assert relative_l2(reduced, numpy_vit(config, tensors, image, bf16=True)) <= 1.0e-3
+        gap = relative_l2(reduced, oracle.vit_forward(config, tensors, image))
+        assert 1.0e-3 < gap < 5.0e-2, gap
+        # logits are bf16 values
+        require_exact(bf16_to_float(oracle.round_bf16(reduced)), reduced, "bf16 logits")
 
 
 def test_round_bf16_matches_torch_and_special_values(oracle):
