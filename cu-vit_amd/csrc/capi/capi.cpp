@@ -85,6 +85,33 @@ int check_gelu(const void* input, const void* output, std::int64_t count, bool* 
     return ok();
 }
 
+/// Validation shared by the fp32 and bf16 fused attention; @p empty is set
+/// for a launch with nothing to do.
+int check_attention(const void* qkv, const void* context, int images, int heads, int tokens,
+                    int head_dim, bool* empty) {
+    *empty = images == 0 || heads == 0 || tokens == 0 || head_dim == 0;
+    if (*empty) {
+        return ok();
+    }
+    if (images < 0 || heads < 0 || tokens < 0 || head_dim < 0) {
+        return fail(CUVIT_ERROR_INVALID_ARGUMENT, "Attention extents cannot be negative");
+    }
+    if (qkv == nullptr || context == nullptr) {
+        return fail(CUVIT_ERROR_INVALID_ARGUMENT, "Attention operands cannot be null");
+    }
+    if (!detail::attention_supported(tokens, head_dim)) {
+        return fail(CUVIT_ERROR_INVALID_ARGUMENT,
+                          "Fused attention supports head_dim 64 and at most 256 tokens");
+    }
+    if (((reinterpret_cast<std::uintptr_t>(qkv) | reinterpret_cast<std::uintptr_t>(context)) & 15U) != 0) {
+        return fail(CUVIT_ERROR_INVALID_ARGUMENT, "Fused attention needs 16-byte aligned operands");
+    }
+    if (saturating_product(images, heads) > 65535) {
+        return fail(CUVIT_ERROR_LENGTH, "Fused attention takes at most 65535 (image, head) pairs");
+    }
+    return ok();
+}
+
 int check_broadcast(const void* destination, const void* source, std::int64_t count,
                     std::int64_t destination_stride, int batch, bool* empty) {
     *empty = count == 0 || batch == 0;
@@ -399,27 +426,25 @@ int cuvit_attention_supported(int tokens, int head_dim) {
 
 int cuvit_attention_f32(const float* qkv, float* context, int images, int heads, int tokens,
                         int head_dim, cuvit_stream_t stream) {
-    if (images == 0 || heads == 0 || tokens == 0 || head_dim == 0) {
-        return capi::ok();
-    }
-    if (images < 0 || heads < 0 || tokens < 0 || head_dim < 0) {
-        return capi::fail(CUVIT_ERROR_INVALID_ARGUMENT, "Attention extents cannot be negative");
-    }
-    if (qkv == nullptr || context == nullptr) {
-        return capi::fail(CUVIT_ERROR_INVALID_ARGUMENT, "Attention operands cannot be null");
-    }
-    if (!detail::attention_supported(tokens, head_dim)) {
-        return capi::fail(CUVIT_ERROR_INVALID_ARGUMENT,
-                          "Fused attention supports head_dim 64 and at most 256 tokens");
-    }
-    if (((reinterpret_cast<std::uintptr_t>(qkv) | reinterpret_cast<std::uintptr_t>(context)) & 15U) != 0) {
-        return capi::fail(CUVIT_ERROR_INVALID_ARGUMENT, "Fused attention needs 16-byte aligned operands");
-    }
-    if (capi::saturating_product(images, heads) > 65535) {
-        return capi::fail(CUVIT_ERROR_LENGTH, "Fused attention takes at most 65535 (image, head) pairs");
+    bool empty = false;
+    if (const int s = capi::check_attention(qkv, context, images, heads, tokens, head_dim, &empty);
+        s != CUVIT_OK || empty) {
+        return s;
     }
     return from_hip(detail::attention_f32(qkv, context, images, heads, tokens, head_dim,
                                           capi::as_hip(stream)),
+                    "attention launch");
+}
+
+int cuvit_attention_bf16(const cuvit_bf16* qkv, cuvit_bf16* context, int images, int heads,
+                         int tokens, int head_dim, cuvit_stream_t stream) {
+    bool empty = false;
+    if (const int s = capi::check_attention(qkv, context, images, heads, tokens, head_dim, &empty);
+        s != CUVIT_OK || empty) {
+        return s;
+    }
+    return from_hip(detail::attention_bf16(qkv, context, images, heads, tokens, head_dim,
+                                           capi::as_hip(stream)),
                     "attention launch");
 }
 

@@ -293,9 +293,8 @@ template <typename T> void VisionTransformer::load(const WeightFile& file, Store
 
 template <typename T> void VisionTransformer::reserve_activations(Stored<T>& stored) {
     constexpr bool kFloat = std::is_same_v<T, float>;
-    // Attention runs fused (fp32, no logits buffer) whenever the shape allows.
-    fused_attention_ = kFloat &&
-                       cuvit_attention_supported(config_.token_count(), config_.head_dim()) != 0 &&
+    // Attention runs fused (no logits buffer) whenever the shape allows.
+    fused_attention_ = cuvit_attention_supported(config_.token_count(), config_.head_dim()) != 0 &&
                        static_cast<std::int64_t>(max_batch_) * config_.heads <= 65535;
 
     const Extent images = max_batch_;
@@ -397,12 +396,13 @@ void VisionTransformer::run_block(const BlockWeights& block,
 
     // softmax(Q.K^T / sqrt(head_dim)).V per (image, head) in one fused launch
     // when the shape allows; it is bitwise equal to the three launches.
-    if constexpr (std::is_same_v<T, float>) {
-        if (fused_attention_) {
+    if (fused_attention_) {
+        if constexpr (std::is_same_v<T, float>) {
             throw_on_error(cuvit_attention_f32(stored.qkv, stored.context, batch, heads, token_count,
                                                head_dim, as_c(stream)));
         } else {
-            attention_unfused(stored, batch, stream);
+            throw_on_error(cuvit_attention_bf16(stored.qkv, stored.context, batch, heads,
+                                                token_count, head_dim, as_c(stream)));
         }
     } else {
         attention_unfused(stored, batch, stream);

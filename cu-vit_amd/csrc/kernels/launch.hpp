@@ -87,6 +87,11 @@ hipError_t gemm_bf16(const std::uint16_t* a, const std::uint16_t* b, const float
 bool attention_supported(int tokens, int head_dim);
 hipError_t attention_f32(const float* qkv, float* context, int images, int heads, int tokens,
                          int head_dim, hipStream_t stream);
+/// attention_f32's bf16 twin: bitwise equal to the bf16 GEMM -> softmax ->
+/// GEMM sequence (logits and probabilities rounded to bf16 as stored there).
+bool attention_bf16_supported(int tokens, int head_dim);
+hipError_t attention_bf16(const std::uint16_t* qkv, std::uint16_t* context, int images, int heads,
+                          int tokens, int head_dim, hipStream_t stream);
 
 // Device facts used to shape grids, cached per device.
 int compute_units();

@@ -44,6 +44,7 @@
 // second pass writes the result.
 #include "device_common.hpp"
 #include "launch.hpp"
+#include "softmax_terms.hpp"
 
 #include <cmath>
 
@@ -54,50 +55,11 @@ using namespace cuvit::device;
 
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
-constexpr float kLog2e = 1.4426950408889634F;
 
 /// Terms per lane the register and staged paths hold.
 constexpr int kMaxTerms = 16;
 /// Widest row a 16-lane team takes.
 constexpr int kTeamColumns = 16 * kMaxTerms;
-
-/// exp(x - max).
-__device__ __forceinline__ float shifted_exp(float x, float max) {
-    return __builtin_amdgcn_exp2f((x - max) * kLog2e);
-}
-
-/// All-reduce over a team of L lanes (16: one DPP row; 64: the wavefront).
-template <int L, typename Op> __device__ __forceinline__ float team_allreduce(float value, Op op) {
-    static_assert(L == 16 || L == 64, "teams are 16 or 64 lanes");
-    if constexpr (L == 16) {
-        return row16_allreduce(value, op);
-    } else {
-        return wave_allreduce(value, op);
-    }
-}
-
-/// Softmax of one row whose J terms per lane are in @p x (-inf past the row):
-/// on return x holds the outputs. Team lane @p t holds columns t + L * j.
-template <int L, int J>
-__device__ __forceinline__ void softmax_terms(float (&x)[J], int t, int columns) {
-    float maximum = x[0];
-#pragma unroll
-    for (int j = 1; j < J; ++j) {
-        maximum = fmaxf(maximum, x[j]);
-    }
-    const float row_maximum = team_allreduce<L>(maximum, Max{});
-    float sum = 0.F;
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        x[j] = t + L * j < columns ? shifted_exp(x[j], row_maximum) : 0.F;
-        sum += x[j];
-    }
-    const float inverse = 1.0F / team_allreduce<L>(sum, Sum{});
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        x[j] *= inverse;
-    }
-}
 
 template <typename T, int L, int J>
 __global__ __launch_bounds__(kBlock) void softmax_rows_kernel(const T* input, T* output, int rows,

@@ -164,6 +164,7 @@ _SIGNATURES = {
     "cuvit_convert_bf16_to_f32": (_I, [_P, _P, _L, _P]),
     "cuvit_attention_supported": (_I, [_I, _I]),
     "cuvit_attention_f32": (_I, [_P, _P, _I, _I, _I, _I, _P]),
+    "cuvit_attention_bf16": (_I, [_P, _P, _I, _I, _I, _I, _P]),
     "cuvit_weight_writer_create": (_I, [ctypes.POINTER(_P)]),
     "cuvit_weight_writer_add": (_I, [_P, ctypes.c_char_p, _I, ctypes.POINTER(_L), _P]),
     "cuvit_weight_writer_write": (_I, [_P, ctypes.c_char_p]),
@@ -331,8 +332,8 @@ def attention(qkv, context, images: int, heads: int, tokens: int, head_dim: int,
     [images, tokens, 3, heads, head_dim] projection into
     [images, tokens, heads, head_dim]; an extension replacing the reference's
     three attention launches (vit.cu:205-245) with bitwise the same result."""
-    check(library().cuvit_attention_f32(_ptr(qkv), _ptr(context), images, heads, tokens, head_dim,
-                                        stream_handle(stream)))
+    fn = library().cuvit_attention_bf16 if _bf16(qkv) else library().cuvit_attention_f32
+    check(fn(_ptr(qkv), _ptr(context), images, heads, tokens, head_dim, stream_handle(stream)))
 
 
 class WeightWriter:

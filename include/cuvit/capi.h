@@ -142,6 +142,10 @@ int cuvit_broadcast_f32(float* destination, const float* source, int64_t count,
 int cuvit_attention_supported(int tokens, int head_dim);
 int cuvit_attention_f32(const float* qkv, float* context, int images, int heads, int tokens,
                         int head_dim, cuvit_stream_t stream);
+/* The bf16 twin: the same three launches through the bf16 twins (logits and
+ * probabilities rounded to bf16 where those launches store them), bitwise. */
+int cuvit_attention_bf16(const cuvit_bf16* qkv, cuvit_bf16* context, int images, int heads,
+                         int tokens, int head_dim, cuvit_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * bfloat16 I/O twins. An extension: the reference has no reduced-precision

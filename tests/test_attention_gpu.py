@@ -97,3 +97,87 @@ def test_fused_attention_rows_are_batch_invariant(cuvit, oracle, device):
         cuvit.attention(qkv[i * per_image:(i + 1) * per_image].clone(), one, 1, heads, tokens, HEAD_DIM)
         require_exact(to_host(one), to_host(full[i * tokens * embed:(i + 1) * tokens * embed]),
                       f"image {i} differs alone")
+
+
+# -- bf16 (an extension of the extension) ---------------------------------------
+
+def unfused_bf16(cuvit, qkv, images, heads, tokens, device):
+    """The bf16 model's launch sequence: the bf16 GEMM, softmax and GEMM twins."""
+    embed = heads * HEAD_DIM
+    row = 3 * embed
+    logits = torch.zeros(images * heads * tokens * tokens, device=device, dtype=torch.bfloat16)
+    p = cuvit.gemm_problem(tokens, tokens, HEAD_DIM, cuvit.TRANSPOSED)
+    p.alpha = 1.0 / np.sqrt(np.float32(HEAD_DIM))
+    p.lda, p.ldb, p.ldc = row, row, tokens
+    b = p.batch
+    b.count, b.inner = images * heads, heads
+    b.stride_a, b.stride_b, b.stride_c = HEAD_DIM, HEAD_DIM, tokens * tokens
+    b.outer_stride_a = b.outer_stride_b = tokens * row
+    b.outer_stride_c = heads * tokens * tokens
+    cuvit.gemm(qkv, qkv[embed:], None, logits, p)
+    cuvit.softmax(logits, logits, images * heads * tokens, tokens)
+    context = torch.zeros(images * tokens * embed, device=device, dtype=torch.bfloat16)
+    p = cuvit.gemm_problem(tokens, HEAD_DIM, tokens, cuvit.NO_TRANSPOSE)
+    p.lda, p.ldb, p.ldc = tokens, row, embed
+    b = p.batch
+    b.count, b.inner = images * heads, heads
+    b.stride_a, b.stride_b, b.stride_c = tokens * tokens, HEAD_DIM, HEAD_DIM
+    b.outer_stride_a = heads * tokens * tokens
+    b.outer_stride_b = tokens * row
+    b.outer_stride_c = tokens * embed
+    cuvit.gemm(logits, qkv[2 * embed:], None, context, p)
+    return context
+
+
+def bf16_qkv(oracle, seed, count, device, stddev=1.0):
+    from conftest import bf16_tensor
+
+    return bf16_tensor(oracle.round_bf16(oracle.generator(seed).normal(count, 0.0, stddev)), device)
+
+
+@pytest.mark.parametrize("images,heads,tokens", [(64, 12, 197), (32, 3, 197), (2, 12, 197), (3, 2, 17),
+                                                 (1, 1, 1), (2, 3, 32), (2, 3, 65), (1, 2, 256),
+                                                 (4, 1, 200), (2, 2, 150), (5, 3, 97)])
+def test_fused_attention_bf16_is_bitwise_the_launch_sequence(cuvit, oracle, device, images, heads,
+                                                             tokens):
+    from conftest import bf16_bits
+
+    embed = heads * HEAD_DIM
+    qkv = bf16_qkv(oracle, 7300 + tokens, images * tokens * 3 * embed, device)
+    expected = unfused_bf16(cuvit, qkv, images, heads, tokens, device)
+    context = torch.full((images * tokens * embed,), float("nan"), device=device, dtype=torch.bfloat16)
+    cuvit.attention(qkv, context, images, heads, tokens, HEAD_DIM)
+    require_exact(bf16_bits(context), bf16_bits(expected),
+                  f"bf16 fused attention {images}x{heads}x{tokens} differs from the launch sequence")
+
+
+def test_fused_attention_bf16_rounds_like_the_oracle(cuvit, oracle, device):
+    """Against the oracle's fp32 attention with the bf16 rounding points
+    (logits and probabilities rounded as the model stores them): equal bits
+    except where GPU and CPU sums straddle a bf16 rounding boundary."""
+    from conftest import bf16_bits
+    from oracle import bf16_to_float
+
+    images, heads, tokens = 2, 3, 197
+    embed = heads * HEAD_DIM
+    row = 3 * embed
+    bits = oracle.round_bf16(oracle.generator(7400).normal(images * tokens * row, 0.0, 0.5))
+    values = bf16_to_float(bits).reshape(images, tokens, 3, heads, HEAD_DIM)
+    expected = np.zeros((images, tokens, heads, HEAD_DIM), np.float32)
+    for i in range(images):
+        for h in range(heads):
+            q = np.ascontiguousarray(values[i, :, 0, h])
+            k = np.ascontiguousarray(values[i, :, 1, h])
+            v = np.ascontiguousarray(values[i, :, 2, h])
+            logits = oracle.gemm_transposed(q, k, None, tokens, tokens, HEAD_DIM, np.float32(0.125))
+            logits = bf16_to_float(oracle.round_bf16(logits)).reshape(tokens, tokens)
+            weights = bf16_to_float(oracle.round_bf16(oracle.softmax(logits))).reshape(tokens, tokens)
+            expected[i, :, h] = oracle.gemm(weights, v, None, tokens, HEAD_DIM, tokens).reshape(tokens, HEAD_DIM)
+    from conftest import bf16_tensor
+
+    context = torch.zeros(expected.size, device=device, dtype=torch.bfloat16)
+    cuvit.attention(bf16_tensor(bits, device), context, images, heads, tokens, HEAD_DIM)
+    distance = np.abs(bf16_bits(context).astype(np.int32) -
+                      oracle.round_bf16(expected.reshape(-1)).astype(np.int32))
+    fraction = np.count_nonzero(distance) / distance.size
+    assert fraction <= 1.0e-2, f"{fraction:.2e} of the context differs from the rounded oracle"

@@ -57,6 +57,7 @@ def test_zero_extents_return_before_any_check(lib):
     assert lib.cuvit_attention_f32(None, None, 0, 3, 197, 64, None) == 0
     assert lib.cuvit_attention_f32(None, None, 2, 3, 0, 64, None) == 0
     assert lib.cuvit_broadcast_bf16(None, None, 0, 0, 3, None) == 0
+    assert lib.cuvit_attention_bf16(None, None, 0, 12, 197, 64, None) == 0
     assert lib.cuvit_convert_f32_to_bf16(None, None, 0, None) == 0
     assert lib.cuvit_convert_bf16_to_f32(None, None, 0, None) == 0
 
@@ -99,6 +100,12 @@ def test_zero_extents_return_before_any_check(lib):
     (lambda l: l.cuvit_attention_f32(FAKE, FAKE, 2, 3, 257, 64, None),
      "Fused attention supports head_dim 64 and at most 256 tokens"),
     (lambda l: l.cuvit_attention_f32(FAKE + 4, FAKE, 2, 3, 197, 64, None),
+     "Fused attention needs 16-byte aligned operands"),
+    (lambda l: l.cuvit_attention_bf16(FAKE, FAKE, 2, 3, 197, 32, None),
+     "Fused attention supports head_dim 64 and at most 256 tokens"),
+    (lambda l: l.cuvit_attention_bf16(FAKE, None, 2, 3, 197, 64, None),
+     "Attention operands cannot be null"),
+    (lambda l: l.cuvit_attention_bf16(FAKE + 8, FAKE, 2, 3, 197, 64, None),
      "Fused attention needs 16-byte aligned operands"),
     (lambda l: l.cuvit_broadcast_bf16(FAKE, FAKE, 8, 4, 2, None), "Broadcast extents are inconsistent"),
     (lambda l: l.cuvit_broadcast_bf16(None, FAKE, 4, 8, 2, None), "Broadcast operands cannot be null"),
