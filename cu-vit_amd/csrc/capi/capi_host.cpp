@@ -72,6 +72,17 @@ int cuvit_weight_writer_add(cuvit_weight_writer* writer, const char* name, int r
     });
 }
 
+int cuvit_weight_writer_add_bf16(cuvit_weight_writer* writer, const char* name, int rank,
+                                 const int64_t* extents, const cuvit_bf16* data) {
+    return guarded([&]() -> int {
+        if (writer == nullptr || name == nullptr) {
+            return fail(CUVIT_ERROR_INVALID_ARGUMENT, "writer and name cannot be null");
+        }
+        writer->writer.add_bf16(name, extents_of(rank, extents), data);
+        return CUVIT_OK;
+    });
+}
+
 int cuvit_weight_writer_write(const cuvit_weight_writer* writer, const char* path) {
     return guarded([&]() -> int {
         if (writer == nullptr || path == nullptr) {
@@ -113,6 +124,28 @@ int cuvit_weight_file_float_data(const cuvit_weight_file* file, const char* name
         *data = file->file.float_data(name, extents_of(rank, extents));
         return CUVIT_OK;
     });
+}
+
+int cuvit_weight_file_bf16_data(const cuvit_weight_file* file, const char* name, int rank,
+                                const int64_t* extents, const cuvit_bf16** data) {
+    return guarded([&]() -> int {
+        if (file == nullptr || name == nullptr || data == nullptr) {
+            return fail(CUVIT_ERROR_INVALID_ARGUMENT, "file, name and out-pointer cannot be null");
+        }
+        *data = file->file.bf16_data(name, extents_of(rank, extents));
+        return CUVIT_OK;
+    });
+}
+
+int cuvit_weight_file_version(const cuvit_weight_file* file) {
+    return file == nullptr ? 0 : static_cast<int>(file->file.version());
+}
+
+int cuvit_weight_file_type(const cuvit_weight_file* file, const char* name) {
+    if (file == nullptr || name == nullptr || !file->file.contains(name)) {
+        return 0;
+    }
+    return static_cast<int>(file->file.entry(name).type);
 }
 
 const char* cuvit_weight_file_entry_name(const cuvit_weight_file* file, int64_t index) {

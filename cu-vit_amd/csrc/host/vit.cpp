@@ -71,19 +71,33 @@ class Staging {
         return {device, reinterpret_cast<T*>(host_.data() + offset)};
     }
 
-    /// Stages tensor @p name in storage type T: copied as fp32, or rounded
-    /// to bf16 bits.
+    /// Stages tensor @p name (float32 or, from a version 2 file, bfloat16)
+    /// in storage type T: copied when the types match, else widened exactly
+    /// to fp32 or rounded to bf16 bits.
     template <typename T>
     const T* upload(const WeightFile& file, const std::string& name,
                     const std::vector<Extent>& extents) {
-        const float* const source = file.float_data(name, extents);
+        const bool stored_bf16 = file.entry(name).type == DataType::kBFloat16;
         const auto count = static_cast<std::size_t>(element_count(extents));
         const auto [device, mirror] = carve<T>(count);
         if constexpr (std::is_same_v<T, float>) {
-            std::memcpy(mirror, source, count * sizeof(float));
+            if (stored_bf16) {
+                const std::uint16_t* const source = file.bf16_data(name, extents);
+                for (std::size_t i = 0; i < count; ++i) {
+                    const std::uint32_t widened = static_cast<std::uint32_t>(source[i]) << 16;
+                    std::memcpy(mirror + i, &widened, sizeof(float));
+                }
+            } else {
+                std::memcpy(mirror, file.float_data(name, extents), count * sizeof(float));
+            }
         } else {
-            for (std::size_t i = 0; i < count; ++i) {
-                mirror[i] = round_to_bf16(source[i]);
+            if (stored_bf16) {
+                std::memcpy(mirror, file.bf16_data(name, extents), count * sizeof(std::uint16_t));
+            } else {
+                const float* const source = file.float_data(name, extents);
+                for (std::size_t i = 0; i < count; ++i) {
+                    mirror[i] = round_to_bf16(source[i]);
+                }
             }
         }
         return device;
@@ -275,11 +289,11 @@ template <typename T> void VisionTransformer::load(const WeightFile& file, Store
     // the same rounding as the reference's broadcast-then-add (vit.cu:295-300),
     // then (bf16) one rounding to storage, as every other stored token.
     {
-        const float* const cls = file.float_data("cls_token", {1, 1, embed});
-        const float* const pos = file.float_data("pos_embed", {1, tokens, embed});
+        const std::vector<float> cls = file.values("cls_token", {1, 1, embed});
+        const std::vector<float> pos = file.values("pos_embed", {1, tokens, embed});
         const auto [device, mirror] = staging.carve<T>(static_cast<std::size_t>(embed));
         for (Extent i = 0; i < embed; ++i) {
-            const float sum = cls[i] + pos[i];
+            const float sum = cls[static_cast<std::size_t>(i)] + pos[static_cast<std::size_t>(i)];
             if constexpr (kFloat) {
                 mirror[i] = sum;
             } else {

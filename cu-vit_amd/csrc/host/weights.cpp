@@ -1,6 +1,7 @@
-// .cvw v1 reader and writer (format: include/cuvit/weights.hpp). Byte layout,
+// .cvw reader and writer (format: include/cuvit/weights.hpp). Byte layout,
 // validation and error conditions follow the reference's
-// src/runtime/weights.cpp:13-296 so files move between the two unchanged.
+// src/runtime/weights.cpp:13-296 so version 1 files move between the two
+// unchanged; version 2 adds the bf16 type and nothing else.
 #include "cuvit/weights.hpp"
 
 #include <cstring>
@@ -65,12 +66,17 @@ std::string shape_text(const std::vector<Extent>& extents) {
 } // namespace
 
 const char* data_type_name(DataType type) {
-    return type == DataType::kFloat32 ? "float32" : "unknown";
+    switch (type) {
+    case DataType::kFloat32: return "float32";
+    case DataType::kBFloat16: return "bfloat16";
+    }
+    return "unknown";
 }
 
 std::size_t data_type_size(DataType type) {
-    if (type == DataType::kFloat32) {
-        return sizeof(float);
+    switch (type) {
+    case DataType::kFloat32: return sizeof(float);
+    case DataType::kBFloat16: return sizeof(std::uint16_t);
     }
     throw std::runtime_error("Weight file names an unsupported data type");
 }
@@ -107,10 +113,12 @@ WeightFile WeightFile::load(const std::string& path) {
         throw std::runtime_error("Not a Cu-Vit weight file: " + path);
     }
     const auto version = cursor.scalar<std::uint32_t>();
-    if (version != kVersion) {
+    if (version != kVersion && version != kBFloat16Version) {
         throw std::runtime_error("Weight file " + path + " has version " + std::to_string(version) +
-                                 ", but this build reads version " + std::to_string(kVersion));
+                                 ", but this build reads versions " + std::to_string(kVersion) +
+                                 " and " + std::to_string(kBFloat16Version));
     }
+    file.version_ = version;
     const auto count = cursor.scalar<std::uint32_t>();
     static_cast<void>(cursor.scalar<std::uint32_t>()); // reserved
 
@@ -121,11 +129,14 @@ WeightFile WeightFile::load(const std::string& path) {
         entry.name = cursor.text(cursor.scalar<std::uint32_t>());
 
         const auto type = cursor.scalar<std::uint32_t>();
-        if (type != static_cast<std::uint32_t>(DataType::kFloat32)) {
+        const bool known = type == static_cast<std::uint32_t>(DataType::kFloat32) ||
+                           (version == kBFloat16Version &&
+                            type == static_cast<std::uint32_t>(DataType::kBFloat16));
+        if (!known) {
             throw std::runtime_error("Tensor '" + entry.name + "' has unsupported data type " +
                                      std::to_string(type));
         }
-        entry.type = DataType::kFloat32;
+        entry.type = static_cast<DataType>(type);
 
         const auto rank = cursor.scalar<std::uint32_t>();
         if (rank == 0 || rank > static_cast<std::uint32_t>(kMaxTensorRank)) {
@@ -170,18 +181,50 @@ const WeightEntry& WeightFile::entry(const std::string& name) const {
     return entries_[found->second];
 }
 
-const float* WeightFile::float_data(const std::string& name,
-                                    const std::vector<Extent>& expected_extents) const {
+const WeightEntry& WeightFile::checked(const std::string& name,
+                                       const std::vector<Extent>& expected_extents,
+                                       DataType type) const {
     const WeightEntry& found = entry(name);
-    if (found.type != DataType::kFloat32) {
+    if (found.type != type) {
         throw std::runtime_error("Tensor '" + name + "' is " + data_type_name(found.type) +
-                                 ", not float32");
+                                 ", not " + data_type_name(type));
     }
     if (found.extents != expected_extents) {
         throw std::runtime_error("Tensor '" + name + "' has shape " + found.shape_string() +
                                  ", but " + shape_text(expected_extents) + " was expected");
     }
+    return found;
+}
+
+const float* WeightFile::float_data(const std::string& name,
+                                    const std::vector<Extent>& expected_extents) const {
+    const WeightEntry& found = checked(name, expected_extents, DataType::kFloat32);
     return reinterpret_cast<const float*>(blob_.data() + found.offset);
+}
+
+const std::uint16_t* WeightFile::bf16_data(const std::string& name,
+                                           const std::vector<Extent>& expected_extents) const {
+    const WeightEntry& found = checked(name, expected_extents, DataType::kBFloat16);
+    return reinterpret_cast<const std::uint16_t*>(blob_.data() + found.offset);
+}
+
+std::vector<float> WeightFile::values(const std::string& name,
+                                      const std::vector<Extent>& expected_extents) const {
+    const WeightEntry& found = entry(name);
+    const auto count = static_cast<std::size_t>(found.element_count());
+    std::vector<float> out(count);
+    if (found.type == DataType::kBFloat16) {
+        const std::uint16_t* const bits = bf16_data(name, expected_extents);
+        for (std::size_t i = 0; i < count; ++i) {
+            const std::uint32_t widened = static_cast<std::uint32_t>(bits[i]) << 16;
+            std::memcpy(&out[i], &widened, sizeof(float));
+        }
+    } else if (count > 0) {
+        std::memcpy(out.data(), float_data(name, expected_extents), count * sizeof(float));
+    } else {
+        static_cast<void>(float_data(name, expected_extents)); // shape and type check
+    }
+    return out;
 }
 
 std::uint64_t WeightFile::payload_bytes() const noexcept {
@@ -192,8 +235,8 @@ std::uint64_t WeightFile::payload_bytes() const noexcept {
     return total;
 }
 
-void WeightFileWriter::add(const std::string& name, const std::vector<Extent>& extents,
-                           const float* data) {
+Extent WeightFileWriter::check_new(const std::string& name, const std::vector<Extent>& extents,
+                                   const void* data) const {
     if (name.empty()) {
         throw std::invalid_argument("A weight tensor needs a name");
     }
@@ -215,7 +258,23 @@ void WeightFileWriter::add(const std::string& name, const std::vector<Extent>& e
     if (count > 0 && data == nullptr) {
         throw std::invalid_argument("Tensor '" + name + "' has no data");
     }
-    entries_.push_back(Pending{name, extents, std::vector<float>(data, data + count)});
+    return count;
+}
+
+void WeightFileWriter::add(const std::string& name, const std::vector<Extent>& extents,
+                           const float* data) {
+    const auto count = static_cast<std::size_t>(check_new(name, extents, data));
+    const auto* const bytes = reinterpret_cast<const std::byte*>(data);
+    entries_.push_back(Pending{name, DataType::kFloat32, extents,
+                               std::vector<std::byte>(bytes, bytes + count * sizeof(float))});
+}
+
+void WeightFileWriter::add_bf16(const std::string& name, const std::vector<Extent>& extents,
+                                const std::uint16_t* data) {
+    const auto count = static_cast<std::size_t>(check_new(name, extents, data));
+    const auto* const bytes = reinterpret_cast<const std::byte*>(data);
+    entries_.push_back(Pending{name, DataType::kBFloat16, extents,
+                               std::vector<std::byte>(bytes, bytes + count * sizeof(std::uint16_t))});
 }
 
 void WeightFileWriter::write(const std::string& path) const {
@@ -232,9 +291,11 @@ void WeightFileWriter::write(const std::string& path) const {
     std::vector<std::uint64_t> offsets;
     offsets.reserve(entries_.size());
     std::uint64_t position = next_payload_offset(table);
+    bool reduced = false;
     for (const Pending& e : entries_) {
         offsets.push_back(position);
-        position = next_payload_offset(position + e.data.size() * sizeof(float));
+        position = next_payload_offset(position + e.data.size());
+        reduced = reduced || e.type != DataType::kFloat32;
     }
 
     std::ofstream out(path, std::ios::binary | std::ios::trunc);
@@ -242,20 +303,20 @@ void WeightFileWriter::write(const std::string& path) const {
         throw std::runtime_error("Cannot create weight file: " + path);
     }
     put(out, WeightFile::kMagic);
-    put(out, WeightFile::kVersion);
+    put(out, reduced ? WeightFile::kBFloat16Version : WeightFile::kVersion);
     put(out, static_cast<std::uint32_t>(entries_.size()));
     put(out, std::uint32_t{0});
     for (std::size_t i = 0; i < entries_.size(); ++i) {
         const Pending& e = entries_[i];
         put(out, static_cast<std::uint32_t>(e.name.size()));
         out.write(e.name.data(), static_cast<std::streamsize>(e.name.size()));
-        put(out, static_cast<std::uint32_t>(DataType::kFloat32));
+        put(out, static_cast<std::uint32_t>(e.type));
         put(out, static_cast<std::uint32_t>(e.extents.size()));
         for (const Extent extent : e.extents) {
             put(out, static_cast<std::int64_t>(extent));
         }
         put(out, offsets[i]);
-        put(out, static_cast<std::uint64_t>(e.data.size() * sizeof(float)));
+        put(out, static_cast<std::uint64_t>(e.data.size()));
     }
     for (std::size_t i = 0; i < entries_.size(); ++i) {
         const auto at = static_cast<std::uint64_t>(out.tellp());
@@ -265,7 +326,7 @@ void WeightFileWriter::write(const std::string& path) const {
         const std::vector<char> zeros(offsets[i] - at, '\0');
         out.write(zeros.data(), static_cast<std::streamsize>(zeros.size()));
         out.write(reinterpret_cast<const char*>(entries_[i].data.data()),
-                  static_cast<std::streamsize>(entries_[i].data.size() * sizeof(float)));
+                  static_cast<std::streamsize>(entries_[i].data.size()));
     }
     if (!out) {
         throw std::runtime_error("Failed while writing weight file: " + path);

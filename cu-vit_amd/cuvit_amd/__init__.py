@@ -167,12 +167,16 @@ _SIGNATURES = {
     "cuvit_attention_bf16": (_I, [_P, _P, _I, _I, _I, _I, _P]),
     "cuvit_weight_writer_create": (_I, [ctypes.POINTER(_P)]),
     "cuvit_weight_writer_add": (_I, [_P, ctypes.c_char_p, _I, ctypes.POINTER(_L), _P]),
+    "cuvit_weight_writer_add_bf16": (_I, [_P, ctypes.c_char_p, _I, ctypes.POINTER(_L), _P]),
     "cuvit_weight_writer_write": (_I, [_P, ctypes.c_char_p]),
     "cuvit_weight_writer_destroy": (None, [_P]),
     "cuvit_weight_file_load": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
     "cuvit_weight_file_size": (_L, [_P]),
     "cuvit_weight_file_contains": (_I, [_P, ctypes.c_char_p]),
     "cuvit_weight_file_float_data": (_I, [_P, ctypes.c_char_p, _I, ctypes.POINTER(_L), ctypes.POINTER(_P)]),
+    "cuvit_weight_file_bf16_data": (_I, [_P, ctypes.c_char_p, _I, ctypes.POINTER(_L), ctypes.POINTER(_P)]),
+    "cuvit_weight_file_version": (_I, [_P]),
+    "cuvit_weight_file_type": (_I, [_P, ctypes.c_char_p]),
     "cuvit_weight_file_entry_name": (ctypes.c_char_p, [_P, _L]),
     "cuvit_weight_file_payload_bytes": (ctypes.c_uint64, [_P]),
     "cuvit_weight_file_destroy": (None, [_P]),
@@ -352,6 +356,15 @@ class WeightWriter:
         check(library().cuvit_weight_writer_add(self._handle, name.encode(), data.ndim, extents,
                                                 data.ctypes.data))
 
+    def add_bf16(self, name: str, bits) -> None:
+        """A bfloat16 tensor from its bit patterns (uint16); the file becomes version 2."""
+        import numpy as np
+
+        data = np.ascontiguousarray(bits, dtype=np.uint16)
+        extents = (ctypes.c_int64 * max(data.ndim, 1))(*data.shape)
+        check(library().cuvit_weight_writer_add_bf16(self._handle, name.encode(), data.ndim,
+                                                     extents, data.ctypes.data))
+
     def write(self, path: str) -> None:
         check(library().cuvit_weight_writer_write(self._handle, os.fsencode(path)))
 
@@ -399,6 +412,26 @@ class WeightFile:
         count = int(np.prod(shape)) if len(shape) else 1
         buffer = (ctypes.c_float * count).from_address(pointer.value) if count else []
         return np.array(np.frombuffer(buffer, dtype=np.float32, count=count)).reshape(shape)
+
+    def bf16_data(self, name: str, shape):
+        """The bfloat16 payload's bit patterns (uint16)."""
+        import numpy as np
+
+        extents = (ctypes.c_int64 * max(len(shape), 1))(*shape)
+        pointer = ctypes.c_void_p()
+        check(library().cuvit_weight_file_bf16_data(self._handle, name.encode(), len(shape),
+                                                    extents, ctypes.byref(pointer)))
+        count = int(np.prod(shape)) if len(shape) else 1
+        buffer = (ctypes.c_uint16 * count).from_address(pointer.value) if count else []
+        return np.array(np.frombuffer(buffer, dtype=np.uint16, count=count)).reshape(shape)
+
+    @property
+    def version(self) -> int:
+        return library().cuvit_weight_file_version(self._handle)
+
+    def dtype(self, name: str) -> int:
+        """1 for float32, 2 for bfloat16, 0 when absent."""
+        return library().cuvit_weight_file_type(self._handle, name.encode())
 
     def close(self) -> None:
         if getattr(self, "_handle", None):

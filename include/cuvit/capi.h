@@ -183,6 +183,8 @@ int cuvit_convert_bf16_to_f32(const cuvit_bf16* input, float* output, int64_t co
  * weights.cpp:13-23), little-endian: header {magic "CVIT", version 1, count,
  * reserved}; entries {name_len u32, name, type u32 (1 = float32), rank u32,
  * extents i64[rank], offset u64, bytes u64}; payloads 64-byte aligned.
+ * Version 2 (an extension) is the same layout plus type 2 = bfloat16; the
+ * writer emits it only for a file holding a bf16 tensor.
  * ------------------------------------------------------------------------- */
 typedef struct cuvit_weight_writer cuvit_weight_writer;
 typedef struct cuvit_weight_file cuvit_weight_file;
@@ -191,6 +193,9 @@ typedef struct cuvit_weight_file cuvit_weight_file;
 int cuvit_weight_writer_create(cuvit_weight_writer** writer);
 int cuvit_weight_writer_add(cuvit_weight_writer* writer, const char* name, int rank,
                             const int64_t* extents, const float* data);
+/* A bfloat16 tensor (bit patterns); the file becomes version 2. Extension. */
+int cuvit_weight_writer_add_bf16(cuvit_weight_writer* writer, const char* name, int rank,
+                                 const int64_t* extents, const cuvit_bf16* data);
 int cuvit_weight_writer_write(const cuvit_weight_writer* writer, const char* path);
 void cuvit_weight_writer_destroy(cuvit_weight_writer* writer);
 
@@ -201,6 +206,13 @@ int cuvit_weight_file_contains(const cuvit_weight_file* file, const char* name);
 /* Host pointer to a float32 payload after checking its shape, as float_data(). */
 int cuvit_weight_file_float_data(const cuvit_weight_file* file, const char* name, int rank,
                                  const int64_t* extents, const float** data);
+/* Host pointer to a bfloat16 payload after checking its type and shape. Extension. */
+int cuvit_weight_file_bf16_data(const cuvit_weight_file* file, const char* name, int rank,
+                                const int64_t* extents, const cuvit_bf16** data);
+/* The file's format version (1 or 2), 0 for a null file. */
+int cuvit_weight_file_version(const cuvit_weight_file* file);
+/* Data type of tensor @p name (1 float32, 2 bfloat16), 0 when absent. */
+int cuvit_weight_file_type(const cuvit_weight_file* file, const char* name);
 /* Name of entry @p index; NULL when out of range. Valid while the file lives. */
 const char* cuvit_weight_file_entry_name(const cuvit_weight_file* file, int64_t index);
 uint64_t cuvit_weight_file_payload_bytes(const cuvit_weight_file* file);

@@ -154,3 +154,53 @@ def test_bf16_batch_limits(cuvit, oracle, device, tmp_path):
     with pytest.raises(cuvit.InvalidArgument):
         model.forward(images, logits, 3)
     model.forward(None, None, 0)
+
+
+# -- bf16 weight files (.cvw version 2) -------------------------------------------
+
+MATRICES = ("patch_embed.proj.weight", "attn.qkv.weight", "attn.proj.weight", "mlp.fc1.weight",
+            "mlp.fc2.weight", "head.weight")
+
+
+def write_mixed(cuvit, oracle, tensors, path):
+    """GEMM matrices as bf16 (rounded to nearest-even), everything else fp32."""
+    writer = cuvit.WeightWriter()
+    for name, values in tensors:
+        if name.endswith(MATRICES):
+            writer.add_bf16(name, oracle.round_bf16(values))
+        else:
+            writer.add(name, values)
+    writer.write(path)
+    writer.close()
+
+
+def test_bf16_weight_file_loads_to_the_same_models(cuvit, oracle, device, tmp_path):
+    """A version 2 file with bf16 matrices: the bf16 model gives bitwise the
+    logits it gives from the fp32 file (it rounds at load to the same bits),
+    and the fp32 model bitwise those of an fp32 file holding the widened
+    matrices."""
+    from oracle import bf16_to_float
+
+    config = small_config(cuvit)
+    tensors = random_weights(cuvit, oracle, config, 515)
+    fp32_path = os.path.join(tmp_path, "fp32.cvw")
+    mixed_path = os.path.join(tmp_path, "mixed.cvw")
+    widened_path = os.path.join(tmp_path, "widened.cvw")
+    write_weights(cuvit, tensors, fp32_path)
+    write_mixed(cuvit, oracle, tensors, mixed_path)
+    widened = [(n, bf16_to_float(oracle.round_bf16(v)).reshape(v.shape) if n.endswith(MATRICES) else v)
+               for n, v in tensors]
+    write_weights(cuvit, widened, widened_path)
+    mixed = cuvit.WeightFile(mixed_path)
+    assert mixed.version == 2
+    images = np.concatenate([random_image(oracle, config, 60 + i) for i in range(3)])
+
+    def logits(path_or_file, precision):
+        weights = path_or_file if isinstance(path_or_file, cuvit.WeightFile) else cuvit.WeightFile(path_or_file)
+        model = cuvit.VisionTransformer(config, weights, 3, precision)
+        return forward(model, images, 3, device)
+
+    require_exact(logits(mixed, cuvit.PRECISION_BF16), logits(fp32_path, cuvit.PRECISION_BF16),
+                  "bf16 model: bf16 file vs fp32 file")
+    require_exact(logits(mixed, cuvit.PRECISION_F32), logits(widened_path, cuvit.PRECISION_F32),
+                  "fp32 model: bf16 file vs widened fp32 file")

@@ -1,10 +1,12 @@
-"""The .cvw v1 weight format, on the CPU.
+"""The .cvw weight format, on the CPU.
 
 Mirrors tests/weights_test.cu (round trip, payload alignment, shape mismatch,
 duplicate names, missing / wrong-magic / wrong-version / truncated files) and
 adds interchange with the reference's own src/runtime/weights.cpp, compiled in
 place into oracle/_ref: a file written by either side loads on the other, and
-the two writers produce identical bytes.
+the two writers produce identical bytes. Version 2 (bf16 tensors, an
+extension) round-trips, is written only for files holding a bf16 tensor, and
+is refused by the reference's reader.
 """
 
 from __future__ import annotations
@@ -102,10 +104,12 @@ def test_corrupt_files_are_rejected(cuvit, tmp_path):
     with pytest.raises(cuvit.CuvitError):
         cuvit.WeightFile(str(junk))
 
+    # the reference's test writes kVersion + 1, which here is the bf16
+    # version 2; the first version this library does not know is 3
     versioned = str(tmp_path / "version.cvw")
     _write(cuvit, [("weight", np.ones(4, np.float32))], versioned)
     blob = bytearray(open(versioned, "rb").read())
-    struct.pack_into("<I", blob, 4, 2)
+    struct.pack_into("<I", blob, 4, 3)
     open(versioned, "wb").write(bytes(blob))
     with pytest.raises(cuvit.CuvitError, match="version"):
         cuvit.WeightFile(versioned)
@@ -174,3 +178,85 @@ def test_reference_and_ours_reject_the_same_corruptions(cuvit, reference, tmp_pa
         assert reference.check_weights(path) is not None, f"the reference accepted {label}"
         with pytest.raises(cuvit.CuvitError):
             cuvit.WeightFile(path)
+
+
+# -- version 2: bfloat16 tensors (an extension) ---------------------------------
+
+def _bf16_tensors(oracle):
+    g = oracle.generator(4343)
+    weight = oracle.round_bf16(g.normal(64 * 48, 0.0, 0.2)).reshape(64, 48)
+    bias = g.normal(64, 0.0, 0.1)
+    return weight, bias
+
+
+def test_bf16_round_trip_and_version(cuvit, oracle, tmp_path):
+    from oracle import bf16_to_float
+
+    weight, bias = _bf16_tensors(oracle)
+    specials = np.array([0x0000, 0x8000, 0x7F80, 0xFF80, 0x7FC1, 0x0001, 0x3F80], np.uint16)
+    path = str(tmp_path / "mixed.cvw")
+    writer = cuvit.WeightWriter()
+    writer.add_bf16("fc.weight", weight)
+    writer.add("fc.bias", bias)
+    writer.add_bf16("specials", specials)
+    writer.write(path)
+    blob = open(path, "rb").read()
+    assert struct.unpack_from("<2I", blob, 0) == (0x54495643, 2)
+    loaded = cuvit.WeightFile(path)
+    assert loaded.version == 2
+    assert (loaded.dtype("fc.weight"), loaded.dtype("fc.bias"), loaded.dtype("absent")) == (2, 1, 0)
+    require_exact(loaded.bf16_data("fc.weight", (64, 48)), weight, "bf16 payload")
+    require_exact(loaded.bf16_data("specials", (7,)), specials, "bf16 special values")
+    require_exact(loaded.float_data("fc.bias", (64,)), bias, "float32 payload in a version 2 file")
+    assert loaded.payload_bytes() == weight.size * 2 + bias.size * 4 + specials.size * 2
+    with pytest.raises(cuvit.CuvitError, match="bfloat16, not float32"):
+        loaded.float_data("fc.weight", (64, 48))
+    with pytest.raises(cuvit.CuvitError, match="float32, not bfloat16"):
+        loaded.bf16_data("fc.bias", (64,))
+    with pytest.raises(cuvit.CuvitError, match="shape"):
+        loaded.bf16_data("fc.weight", (48, 64))
+    # payloads stay 64-byte aligned with 2-byte elements
+    count = struct.unpack_from("<I", blob, 8)[0]
+    cursor = 16
+    for _ in range(count):
+        (length,) = struct.unpack_from("<I", blob, cursor)
+        cursor += 4 + length
+        _, rank = struct.unpack_from("<2I", blob, cursor)
+        cursor += 8 + 8 * rank
+        offset, _ = struct.unpack_from("<2Q", blob, cursor)
+        cursor += 16
+        assert offset % 64 == 0
+    assert np.isnan(bf16_to_float(specials[4:5]))[0]
+
+
+def test_float32_only_files_stay_version_1(cuvit, oracle, tmp_path):
+    path = str(tmp_path / "plain.cvw")
+    _write(cuvit, _tensors(oracle), path)
+    assert struct.unpack_from("<2I", open(path, "rb").read(), 0) == (0x54495643, 1)
+    assert cuvit.WeightFile(path).version == 1
+
+
+def test_bf16_type_is_refused_in_a_version_1_file(cuvit, oracle, tmp_path):
+    weight, _ = _bf16_tensors(oracle)
+    path = str(tmp_path / "v2.cvw")
+    writer = cuvit.WeightWriter()
+    writer.add_bf16("w", weight)
+    writer.write(path)
+    blob = bytearray(open(path, "rb").read())
+    struct.pack_into("<I", blob, 4, 1)
+    open(path, "wb").write(bytes(blob))
+    with pytest.raises(cuvit.CuvitError, match="unsupported data type 2"):
+        cuvit.WeightFile(path)
+
+
+def test_reference_refuses_version_2_and_reads_version_1(cuvit, oracle, reference, tmp_path):
+    """A bf16 file is version 2, which the reference's reader refuses by its
+    version check (weights.cpp:105-109) instead of misreading it."""
+    weight, bias = _bf16_tensors(oracle)
+    path = str(tmp_path / "v2.cvw")
+    writer = cuvit.WeightWriter()
+    writer.add_bf16("w", weight)
+    writer.add("b", bias)
+    writer.write(path)
+    message = reference.check_weights(path)
+    assert message is not None and "version" in message
