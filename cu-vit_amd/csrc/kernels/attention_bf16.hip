@@ -20,15 +20,24 @@
 //     token count contributing exact zeros (the GEMM runs its 64-key stages
 //     in pairs, and so does this loop), then the sum rounded to bf16.
 //
+// The logits and probabilities never touch LDS. A lane of a 32 x 32 logits
+// tile holds query row l % 32 and, for each of four runs q, the keys
+// 8 q + 4 (l / 32) + 0..3, so the two lanes l and l ^ 32 hold a query's whole
+// row. The bf16 softmax's team lane t (column c on lane c % 16, its columns
+// summed in order c = t, t + 16, ...) corresponds to residue t = 8 (q % 2) +
+// 4 (l / 32) + r of a lane's runs: each lane keeps eight of the sixteen
+// partial sums in the same order, the DPP tree (t ^ 1, t ^ 2, half-row
+// mirror, row mirror) becomes (Q0 + Q1) + (Q2 + Q3) over the quad totals Qa
+// with one exchange between l and l ^ 32, and the probabilities, rounded to
+// bf16, are swapped by halves between l and l ^ 32 into the weights.V A
+// fragments (8 consecutive keys per lane).
+//
 // Layout: qkv is [images, tokens, 3, heads, 64] and context is
 // [images, tokens, heads, 64], bf16. A workgroup owns one (image, head) and
 // `waves` query tiles of 32 rows, one per wavefront. V of the (image, head)
-// sits in LDS transposed, [64][keys], so a lane's weights.V B fragment is
-// 16 contiguous bytes; each wavefront keeps its tile's logits, then
-// probabilities, in a private [32][keys] LDS block. Q and K fragments are
-// read straight from global memory (16 contiguous bytes each). Rows are
-// padded by 8 elements, which makes the 16-byte fragment reads of 16
-// consecutive rows hit distinct bank quads for every padded key count.
+// sits in LDS transposed, [64][keys + 8], so a lane's weights.V B fragment is
+// 16 contiguous bytes and 16 consecutive rows hit distinct bank quads; Q and
+// K fragments are read straight from global memory (16 contiguous bytes).
 #include "device_common.hpp"
 #include "gemm_kernel.hpp"
 #include "launch.hpp"
@@ -48,18 +57,17 @@ using Acc = Bf16Mma::Acc;
 constexpr int kHeadDim = 64;
 constexpr int kEdge = 32;        // MFMA tile edge: 32 queries x 32 keys (or dims)
 constexpr int kKBlock = 16;      // k per MFMA
-constexpr int kStage = 64;       // the GEMM's k stage: weights.V runs whole stages
+constexpr int kStage = 64;       // the GEMM's k stage
 constexpr int kMaxTokens = 256;
+constexpr int kMaxKeyTiles = kMaxTokens / kEdge;
 constexpr int kMaxWaves = 8;
-constexpr std::size_t kMaxLds = 152 * 1024; // 256 tokens fit with 7 query tiles
+constexpr int kWavesPerGroup = 4;
 
-/// Elements per padded LDS row for @p tokens keys.
-__host__ __device__ constexpr int row_pitch(int tokens) {
-    return (tokens + kEdge - 1) / kEdge * kEdge + 8;
-}
+/// Elements per LDS row of transposed V for @p key_tiles 32-key tiles.
+__host__ __device__ constexpr int row_pitch(int key_tiles) { return key_tiles * kEdge + 8; }
 
-__host__ __device__ constexpr std::size_t lds_bytes(int tokens, int waves) {
-    return static_cast<std::size_t>(kHeadDim + waves * kEdge) * row_pitch(tokens) * 2;
+__host__ __device__ constexpr std::size_t lds_bytes(int key_tiles) {
+    return static_cast<std::size_t>(kHeadDim) * row_pitch(key_tiles) * 2;
 }
 
 /// 16 bytes at @p element of @p base, or zero when @p inside is false.
@@ -68,20 +76,31 @@ __device__ __forceinline__ Vec16 load_or_zero(const std::uint16_t* base, std::in
     return inside ? load16(base + element) : Vec16{{0U, 0U, 0U, 0U}};
 }
 
-template <int J>
+__device__ __forceinline__ float exchange(float value) { return __shfl_xor(value, 32, kWave); }
+__device__ __forceinline__ std::uint32_t exchange(std::uint32_t value) {
+    return static_cast<std::uint32_t>(__shfl_xor(static_cast<int>(value), 32, kWave));
+}
+
+__device__ __forceinline__ std::uint32_t pack_bf16(float low, float high) {
+    return static_cast<std::uint32_t>(float_to_bf16(low)) |
+           (static_cast<std::uint32_t>(float_to_bf16(high)) << 16);
+}
+
+/// @tparam KT 32-key tiles covering the tokens.
+template <int KT>
 __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
     const std::uint16_t* __restrict__ qkv, std::uint16_t* __restrict__ context, int heads,
     int tokens, float scale) {
+    constexpr int kPadded = KT * kEdge;
+    constexpr int kPitch = row_pitch(KT);
     extern __shared__ Vec16 lds_vectors[];
-    const int pitch = row_pitch(tokens);
-    const int padded = pitch - 8; // keys rounded up to whole 32-key tiles
-    std::uint16_t* const values = reinterpret_cast<std::uint16_t*>(lds_vectors); // [64][pitch]
+    std::uint16_t* const values = reinterpret_cast<std::uint16_t*>(lds_vectors); // [64][kPitch]
     const int waves = static_cast<int>(blockDim.x) / kWave;
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     const int lane = lane_id();
-    const int row = lane % kEdge;         // fragment row
-    const int chunk = 8 * (lane / kEdge); // fragment k offset
-    std::uint16_t* const tile = values + (kHeadDim + wave * kEdge) * pitch; // [32][pitch]
+    const int row = lane % kEdge;  // fragment row: query (logits) or dim (V)
+    const int half = lane / kEdge; // which half of a run pair the lane holds
+    const int chunk = 8 * half;    // fragment k offset
 
     const int pair = blockIdx.y;
     const int image = pair / heads;
@@ -95,139 +114,174 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
 
     // V transposed into LDS; keys past the tokens are zero.
     constexpr int kChunks = kHeadDim / 8;
-    for (int c = threadIdx.x; c < padded * kChunks; c += blockDim.x) {
+    for (int c = threadIdx.x; c < kPadded * kChunks; c += blockDim.x) {
         const int key = c / kChunks;
         const int d0 = 8 * (c % kChunks);
         const Vec16 v = load_or_zero(v_base, key * qkv_row + d0, key < tokens);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            Elem<std::uint16_t>::store_bits(values + (d0 + e) * pitch + key, v, e);
+            Elem<std::uint16_t>::store_bits(values + (d0 + e) * kPitch + key, v, e);
         }
     }
-
+    __syncthreads();
     const int query0 = (static_cast<int>(blockIdx.x) * waves + wave) * kEdge;
-    const bool active = query0 < tokens; // idle waves still meet every barrier
+    if (query0 >= tokens) {
+        return; // no barrier follows
+    }
+    const int query = query0 + row;
 
-    // Logits: 32 queries x 32 keys per MFMA tile, rounded to bf16 into the
-    // wavefront's LDS block.
-    if (active) {
-        const int query = query0 + row;
-        Vec16 q[kHeadDim / kKBlock];
+    // Logits tiles: the GEMM's MFMA and operand roles, alpha * sum rounded
+    // to bf16 as the GEMM stores it, then read back as the softmax reads it.
+    Vec16 q[kHeadDim / kKBlock];
+#pragma unroll
+    for (int kb = 0; kb < kHeadDim / kKBlock; ++kb) {
+        q[kb] = load_or_zero(q_base, query * qkv_row + kb * kKBlock + chunk, query < tokens);
+    }
+    Acc x[KT];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+        const int key = kt * kEdge + row;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            x[kt][i] = 0.F;
+        }
 #pragma unroll
         for (int kb = 0; kb < kHeadDim / kKBlock; ++kb) {
-            q[kb] = load_or_zero(q_base, query * qkv_row + kb * kKBlock + chunk, query < tokens);
+            const Vec16 k = load_or_zero(k_base, key * qkv_row + kb * kKBlock + chunk, key < tokens);
+            Bf16Mma::run(x[kt], k, q[kb]);
         }
-        for (int key0 = 0; key0 < padded; key0 += kEdge) {
-            const int key = key0 + row;
-            Acc acc;
+    }
+
+    // Row max over the valid keys (exact in any order).
+    float maximum = -INFINITY;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                acc[r] = 0.F;
-            }
+    for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
-            for (int kb = 0; kb < kHeadDim / kKBlock; ++kb) {
-                const Vec16 k =
-                    load_or_zero(k_base, key * qkv_row + kb * kKBlock + chunk, key < tokens);
-                Bf16Mma::run(acc, k, q[kb]);
+        for (int i = 0; i < 16; ++i) {
+            const int key = kt * kEdge + Bf16Mma::column(lane, i / 4) + i % 4;
+            x[kt][i] = bf16_to_float(float_to_bf16(scale * x[kt][i]));
+            if (key < tokens) {
+                maximum = fmaxf(maximum, x[kt][i]);
             }
-            // lane: query row, keys key0 + column(lane, run) + 0..3
+        }
+    }
+    maximum = fmaxf(maximum, exchange(maximum));
+
+    // Exponentials; keys past the tokens are 0, as the softmax sets them.
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int key = kt * kEdge + Bf16Mma::column(lane, i / 4) + i % 4;
+            x[kt][i] = key < tokens ? shifted_exp(x[kt][i], maximum) : 0.F;
+        }
+    }
+
+    // Team lane t = 8 g + 4 half + r sums columns t + 16 j, j = 0, 1, ...:
+    // column t + 16 j is run q = g + 2 (j % 2), element r, of key tile j / 2.
+    float quad[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        float part[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float sum = 0.F;
+#pragma unroll
+            for (int j = 0; j < 2 * KT; ++j) {
+                sum += x[j / 2][4 * (g + 2 * (j % 2)) + r];
+            }
+            part[r] = sum;
+        }
+        // DPP steps t ^ 1 and t ^ 2 inside the quad
+        quad[g] = (part[0] + part[1]) + (part[2] + part[3]);
+    }
+    // half-row mirror pairs quads 0-1 and 2-3, row mirror the two results:
+    // (Q0 + Q1) + (Q2 + Q3), the same bits in both lanes of the row
+    const float total = (quad[0] + exchange(quad[0])) + (quad[1] + exchange(quad[1]));
+    const float inverse = 1.0F / total;
+
+    // Probabilities rounded to bf16 and packed by runs: p[kt][q] = keys
+    // kt * 32 + 8 q + 4 half + 0..3.
+    std::uint32_t p[KT][4][2];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+        for (int run = 0; run < 4; ++run) {
+            p[kt][run][0] = pack_bf16(x[kt][4 * run] * inverse, x[kt][4 * run + 1] * inverse);
+            p[kt][run][1] = pack_bf16(x[kt][4 * run + 2] * inverse, x[kt][4 * run + 3] * inverse);
+        }
+    }
+    // A fragment of k-block 2 kt + s: keys kt * 32 + 16 s + 8 half + 0..7,
+    // runs 2 s + half's two halves: the lane's own half and its partner's.
+    Vec16 fragment[2 * KT];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const std::uint32_t send0 = half ? p[kt][2 * s][0] : p[kt][2 * s + 1][0];
+            const std::uint32_t send1 = half ? p[kt][2 * s][1] : p[kt][2 * s + 1][1];
+            const std::uint32_t own0 = half ? p[kt][2 * s + 1][0] : p[kt][2 * s][0];
+            const std::uint32_t own1 = half ? p[kt][2 * s + 1][1] : p[kt][2 * s][1];
+            const std::uint32_t got0 = exchange(send0);
+            const std::uint32_t got1 = exchange(send1);
+            Vec16& f = fragment[2 * kt + s];
+            f.w[0] = half ? got0 : own0;
+            f.w[1] = half ? got1 : own1;
+            f.w[2] = half ? own0 : got0;
+            f.w[3] = half ? own1 : got1;
+        }
+    }
+
+    // weights.V over the GEMM's k-blocks: its 64-key stages run in pairs.
+    constexpr int kStages = (kPadded + kStage - 1) / kStage;
+    constexpr int kBlocks = (kStages + 1) / 2 * 2 * (kStage / kKBlock);
+#pragma unroll
+    for (int d0 = 0; d0 < kHeadDim; d0 += kEdge) {
+        Acc acc;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            acc[i] = 0.F;
+        }
+#pragma unroll
+        for (int kb = 0; kb < kBlocks; ++kb) {
+            if (kb < 2 * KT) {
+                const Vec16 v = load16(values + (d0 + row) * kPitch + kb * kKBlock + chunk);
+                Bf16Mma::run(acc, v, fragment[kb]);
+            } else {
+                const Vec16 zero{{0U, 0U, 0U, 0U}};
+                Bf16Mma::run(acc, zero, zero);
+            }
+        }
+        if (query < tokens) {
+            std::uint16_t* const out = context +
+                                       (static_cast<std::int64_t>(image) * tokens + query) * embed +
+                                       head * kHeadDim + d0;
 #pragma unroll
             for (int run = 0; run < Bf16Mma::kRuns; ++run) {
-                const int column = key0 + Bf16Mma::column(lane, run);
                 uint2 bits;
-                bits.x = static_cast<std::uint32_t>(float_to_bf16(scale * acc[4 * run])) |
-                         (static_cast<std::uint32_t>(float_to_bf16(scale * acc[4 * run + 1])) << 16);
-                bits.y = static_cast<std::uint32_t>(float_to_bf16(scale * acc[4 * run + 2])) |
-                         (static_cast<std::uint32_t>(float_to_bf16(scale * acc[4 * run + 3])) << 16);
-                *reinterpret_cast<uint2*>(tile + row * pitch + column) = bits;
-            }
-        }
-    }
-    __syncthreads();
-
-    // Softmax of the wavefront's 32 rows, four 16-lane teams at a time;
-    // probabilities go back in place, keys past the tokens as zero.
-    if (active) {
-        const int t = lane % 16;
-        for (int base = 0; base < kEdge; base += kWave / 16) {
-            std::uint16_t* const r = tile + (base + lane / 16) * pitch;
-            float x[J];
-#pragma unroll
-            for (int j = 0; j < J; ++j) {
-                const int column = t + 16 * j;
-                x[j] = column < tokens ? bf16_to_float(r[column]) : -INFINITY;
-            }
-            softmax_terms<16, J>(x, t, tokens);
-#pragma unroll
-            for (int j = 0; j < J; ++j) {
-                const int column = t + 16 * j;
-                if (column < padded) {
-                    r[column] = float_to_bf16(x[j]);
-                }
-            }
-            for (int column = 16 * J + t; column < padded; column += 16) {
-                r[column] = 0;
-            }
-        }
-    }
-    __syncthreads();
-
-    // weights.V: two 32-wide tiles of head_dim, k over whole 64-key stages.
-    if (active) {
-        const int query = query0 + row;
-        // the GEMM's loop runs its stages in pairs (a stage past K adds
-        // products 0 * 0), so the same number of k-blocks runs here
-        const int stages = (tokens + kStage - 1) / kStage;
-        const int k_blocks = (stages + 1) / 2 * 2 * (kStage / kKBlock);
-#pragma unroll
-        for (int d0 = 0; d0 < kHeadDim; d0 += kEdge) {
-            Acc acc;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                acc[r] = 0.F;
-            }
-            for (int kb = 0; kb < k_blocks; ++kb) {
-                const int key = kb * kKBlock + chunk;
-                const bool inside = key < padded;
-                const Vec16 p = inside ? load16(tile + row * pitch + key) : Vec16{{0U, 0U, 0U, 0U}};
-                const Vec16 v =
-                    inside ? load16(values + (d0 + row) * pitch + key) : Vec16{{0U, 0U, 0U, 0U}};
-                Bf16Mma::run(acc, v, p);
-            }
-            if (query < tokens) {
-                std::uint16_t* const out = context +
-                                           (static_cast<std::int64_t>(image) * tokens + query) * embed +
-                                           head * kHeadDim + d0;
-#pragma unroll
-                for (int run = 0; run < Bf16Mma::kRuns; ++run) {
-                    const int column = Bf16Mma::column(lane, run);
-                    uint2 bits;
-                    bits.x = static_cast<std::uint32_t>(float_to_bf16(1.0F * acc[4 * run])) |
-                             (static_cast<std::uint32_t>(float_to_bf16(1.0F * acc[4 * run + 1])) << 16);
-                    bits.y = static_cast<std::uint32_t>(float_to_bf16(1.0F * acc[4 * run + 2])) |
-                             (static_cast<std::uint32_t>(float_to_bf16(1.0F * acc[4 * run + 3])) << 16);
-                    *reinterpret_cast<uint2*>(out + column) = bits;
-                }
+                bits.x = pack_bf16(1.0F * acc[4 * run], 1.0F * acc[4 * run + 1]);
+                bits.y = pack_bf16(1.0F * acc[4 * run + 2], 1.0F * acc[4 * run + 3]);
+                *reinterpret_cast<uint2*>(out + Bf16Mma::column(lane, run)) = bits;
             }
         }
     }
 }
 
-template <int J>
+template <int KT>
 hipError_t launch(const std::uint16_t* qkv, std::uint16_t* context, int images, int heads,
-                  int tokens, int waves, hipStream_t stream) {
-    auto kernel = attention_bf16_kernel<J>;
-    static std::atomic<std::uint64_t> opted_in{0};
-    if (const hipError_t opted = allow_lds(reinterpret_cast<const void*>(kernel), kMaxLds, opted_in);
-        opted != hipSuccess) {
-        return opted;
-    }
+                  int tokens, hipStream_t stream) {
+    // Four query tiles per workgroup: measured against 1, 2, 3 and 7 on
+    // MI355X, it was fastest or within 3% at 197 tokens for 12 to 768
+    // (image, head) pairs (ViT-Tiny b32: 13.1 us against 18.7 with all seven
+    // tiles in one workgroup; ViT-Base b64: 56.7 against 55.2).
     const int query_tiles = (tokens + kEdge - 1) / kEdge;
+    const std::int64_t pairs = static_cast<std::int64_t>(images) * heads;
+    const int waves = query_tiles < kWavesPerGroup ? query_tiles : kWavesPerGroup;
     const dim3 grid(static_cast<unsigned int>((query_tiles + waves - 1) / waves),
-                    static_cast<unsigned int>(images * heads));
+                    static_cast<unsigned int>(pairs));
     const float scale = 1.0F / std::sqrt(static_cast<float>(kHeadDim));
-    kernel<<<grid, waves * kWave, lds_bytes(tokens, waves), stream>>>(qkv, context, heads, tokens,
-                                                                       scale);
+    attention_bf16_kernel<KT><<<grid, waves * kWave, lds_bytes(KT), stream>>>(qkv, context, heads,
+                                                                               tokens, scale);
     return hipGetLastError();
 }
 
@@ -242,35 +296,15 @@ hipError_t attention_bf16(const std::uint16_t* qkv, std::uint16_t* context, int 
     if (!attention_bf16_supported(tokens, head_dim)) {
         return hipErrorInvalidValue;
     }
-    // Query tiles per workgroup: as many as LDS holds, fewer when that would
-    // leave the grid under two workgroups per compute unit.
-    const int query_tiles = (tokens + kEdge - 1) / kEdge;
-    const std::int64_t pairs = static_cast<std::int64_t>(images) * heads;
-    int waves = query_tiles < kMaxWaves ? query_tiles : kMaxWaves;
-    while (waves > 1 && lds_bytes(tokens, waves) > kMaxLds) {
-        --waves;
-    }
-    const std::int64_t target = 2 * static_cast<std::int64_t>(compute_units());
-    while (waves > 1 && pairs * ((query_tiles + waves - 1) / waves) < target) {
-        --waves;
-    }
-    // J as the bf16 softmax picks it for rows of `tokens` (any J that covers
-    // the row gives the same bits).
-    switch ((tokens + 15) / 16) {
-    case 1:
-    case 2: return launch<2>(qkv, context, images, heads, tokens, waves, stream);
-    case 3:
-    case 4: return launch<4>(qkv, context, images, heads, tokens, waves, stream);
-    case 5:
-    case 6:
-    case 7:
-    case 8: return launch<8>(qkv, context, images, heads, tokens, waves, stream);
-    case 9:
-    case 10:
-    case 11:
-    case 12:
-    case 13: return launch<13>(qkv, context, images, heads, tokens, waves, stream);
-    default: return launch<16>(qkv, context, images, heads, tokens, waves, stream);
+    switch ((tokens + kEdge - 1) / kEdge) {
+    case 1: return launch<1>(qkv, context, images, heads, tokens, stream);
+    case 2: return launch<2>(qkv, context, images, heads, tokens, stream);
+    case 3: return launch<3>(qkv, context, images, heads, tokens, stream);
+    case 4: return launch<4>(qkv, context, images, heads, tokens, stream);
+    case 5: return launch<5>(qkv, context, images, heads, tokens, stream);
+    case 6: return launch<6>(qkv, context, images, heads, tokens, stream);
+    case 7: return launch<7>(qkv, context, images, heads, tokens, stream);
+    default: return launch<kMaxKeyTiles>(qkv, context, images, heads, tokens, stream);
     }
 }
 
