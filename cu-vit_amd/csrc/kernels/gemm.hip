@@ -7,7 +7,8 @@
 //        a problem has work for more than 32 small tiles per compute unit.
 //   bf16 (32 x 32 MFMA): 128 x 128 once a problem fills every compute unit
 //        twice with it (ViT-Base FC2 12608 x 768 x 3072: 118 us against
-//        130 us for 64 x 64), else 64 x 64.
+//        130 us for 64 x 64), else 64 x 64; 128 x 128 with 32-deep stages
+//        up to K = 1024.
 // Both tiles of a type run the same MFMA over K in the same order, so the
 // choice never changes a result.
 #include "gemm_kernel.hpp"
@@ -72,7 +73,8 @@ gemm::TileMap tile_map(const GemmArgs& args, int bm, int bn, std::size_t element
     return map;
 }
 
-template <typename T, int WM, int WN, int TM, int TN, int BK, bool VecA, bool VecB, bool TransB>
+template <typename T, int WM, int WN, int TM, int TN, int BK, int MinWaves, bool VecA, bool VecB,
+          bool TransB>
 hipError_t launch(const T* a, const T* b, const float* bias, T* c, const GemmArgs& args,
                   bool vector_c, hipStream_t stream) {
     using S = Shape<T, WM, WN, TM, TN, BK>;
@@ -87,7 +89,7 @@ hipError_t launch(const T* a, const T* b, const float* bias, T* c, const GemmArg
     if (tiles > 0x7FFFFFFF) {
         return hipErrorInvalidConfiguration;
     }
-    auto kernel = gemm::gemm_kernel<T, WM, WN, TM, TN, BK, VecA, VecB, TransB>;
+    auto kernel = gemm::gemm_kernel<T, WM, WN, TM, TN, BK, VecA, VecB, TransB, MinWaves>;
     // Above 64 KiB of LDS a kernel has to opt in, once per device.
     static std::atomic<std::uint64_t> opted_in{0};
     if (const hipError_t opted = allow_lds(reinterpret_cast<const void*>(kernel), S::kLdsBytes, opted_in);
@@ -100,7 +102,7 @@ hipError_t launch(const T* a, const T* b, const float* bias, T* c, const GemmArg
     return hipGetLastError();
 }
 
-template <typename T, int WM, int WN, int TM, int TN, int BK>
+template <typename T, int WM, int WN, int TM, int TN, int BK, int MinWaves = 1>
 hipError_t pick_flags(const T* a, const T* b, const float* bias, T* c, const GemmArgs& args,
                       hipStream_t stream) {
     using S = Shape<T, WM, WN, TM, TN, BK>;
@@ -118,8 +120,9 @@ hipError_t pick_flags(const T* a, const T* b, const float* bias, T* c, const Gem
     }
     const bool vec_c = vector_output(c, args);
 #define CUVIT_GEMM_LAUNCH(VA, VB)                                                                  \
-    (args.transposed ? launch<T, WM, WN, TM, TN, BK, VA, VB, true>(a, b, bias, c, args, vec_c, stream) \
-                     : launch<T, WM, WN, TM, TN, BK, VA, VB, false>(a, b, bias, c, args, vec_c, stream))
+    (args.transposed                                                                               \
+         ? launch<T, WM, WN, TM, TN, BK, MinWaves, VA, VB, true>(a, b, bias, c, args, vec_c, stream) \
+         : launch<T, WM, WN, TM, TN, BK, MinWaves, VA, VB, false>(a, b, bias, c, args, vec_c, stream))
     if (vec_a) {
         return vec_b ? CUVIT_GEMM_LAUNCH(true, true) : CUVIT_GEMM_LAUNCH(true, false);
     }
@@ -144,6 +147,13 @@ hipError_t gemm_f32(const float* a, const float* b, const float* bias, float* c,
 hipError_t gemm_bf16(const std::uint16_t* a, const std::uint16_t* b, const float* bias,
                      std::uint16_t* c, const GemmArgs& args, hipStream_t stream) {
     if (tile_count(args, 128, 128) >= static_cast<std::int64_t>(compute_units()) * 2) {
+        // Up to K = 1024, 32-deep stages with registers for three workgroups
+        // per CU beat 64-deep ones at two (ViT-Base FC1 + GELU 146 -> 136 us,
+        // QKV 103 -> 96, projection 45.5 -> 38.4); FC2 (K = 3072) keeps the
+        // 64-deep stages (95 against 99 us).
+        if (args.k <= 1024) {
+            return pick_flags<std::uint16_t, 2, 2, 2, 2, 32, 3>(a, b, bias, c, args, stream);
+        }
         return pick_flags<std::uint16_t, 2, 2, 2, 2, 64>(a, b, bias, c, args, stream);
     }
     return pick_flags<std::uint16_t, 2, 2, 1, 1, 64>(a, b, bias, c, args, stream);

@@ -33,8 +33,9 @@
 // contiguous bytes at a time.
 //
 // Determinism. Every tile shape of a type uses the same MFMA and walks K in
-// the same order with no split-K, so an output element is computed by the
-// same operations whatever the tile, the problem height or the batch. That
+// the same order, over the same number of k-blocks, with no split-K, so an
+// output element is computed by the same operations whatever the tile, the
+// problem height or the batch. That
 // keeps results independent of the tile choice (the property the reference
 // states at gemm.cu:233-235) and batched rows bitwise equal to the same rows
 // computed alone. Operand elements outside the problem read as zero, so
@@ -239,8 +240,17 @@ struct TileMap {
 /// Start of part @p i of @p n split into @p parts near-equal parts.
 __device__ __forceinline__ int split_point(int n, int parts, int i) { return n * i / parts; }
 
-template <typename T, int WM, int WN, int TM, int TN, int BK, bool VecA, bool VecB, bool TransB>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(const T* __restrict__ a,
+/// K walked per type in whole spans: every tile shape of a type runs the same
+/// number of k-blocks (those past K add 0 * 0), so even the sign of an exact
+/// zero result does not depend on the tile. fp32 stages are 32 deep and run
+/// in pairs; bf16 stages are 32 or 64 deep and run to a multiple of 128.
+template <typename T> constexpr int kSpan = sizeof(T) == 2 ? 128 : 64;
+
+/// @tparam MinWaves wavefronts per SIMD the register allocation must allow
+/// (amdgpu_waves_per_eu); 1 leaves the compiler free.
+template <typename T, int WM, int WN, int TM, int TN, int BK, bool VecA, bool VecB, bool TransB,
+          int MinWaves>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(MinWaves))) void gemm_kernel(const T* __restrict__ a,
                                                         const T* __restrict__ b,
                                                         const float* __restrict__ bias, T* c,
                                                         GemmArgs args, TileMap map, bool vector_c) {
@@ -284,7 +294,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const T* __restrict__ a,
     }
     const int row0 = tile_m * BM;
     const int col0 = tile_n * BN;
-    const int steps = (args.k + BK - 1) / BK;
+    static_assert(kSpan<T> % (2 * BK) == 0, "a span is a whole number of stage pairs");
+    const int steps = (args.k + kSpan<T> - 1) / kSpan<T> * (kSpan<T> / BK);
 
     for (int entry = blockIdx.y; entry < args.count; entry += gridDim.y) {
         const Offsets off = entry_offsets(args, entry);
