@@ -1,9 +1,10 @@
 // C++ tests of the host-side plumbing and launcher API, one executable with two
 // groups: `host` needs no GPU (TensorView, launcher validation and exception
 // mapping, weight files, VitConfig, arena sizing); `device` needs one
-// (DeviceBuffer, HostBuffer, Stream, DeviceArena). The cases follow the
-// reference's tests/tensor_test.cu, device_buffer_test.cu, host_buffer_test.cu,
-// stream_test.cu, device_arena_test.cu and weights_test.cu.
+// (DeviceBuffer, HostBuffer, Stream, DeviceArena, and VisionTransformer in
+// both precisions through the C++ API). The cases follow the reference's
+// tests/tensor_test.cu, device_buffer_test.cu, host_buffer_test.cu,
+// stream_test.cu, device_arena_test.cu, weights_test.cu and vit_test.cu.
 #include "cuvit/device_arena.hpp"
 #include "cuvit/device_buffer.hpp"
 #include "cuvit/hip_check.hpp"
@@ -401,6 +402,127 @@ void arena_carving() {
     require(arena.used() == 0 && arena.remaining() == arena.capacity(), "reset");
 }
 
+// -- device: the model through the C++ API (reference vit_test.cu) -----------
+
+/// The vit_test configuration (vit_test.cu:36-47).
+cuvit::VitConfig small_config() {
+    cuvit::VitConfig config;
+    config.image_size = 32;
+    config.patch_size = 8;
+    config.embed_dim = 24;
+    config.depth = 2;
+    config.heads = 4;
+    config.mlp_hidden = 48;
+    config.classes = 7;
+    return config;
+}
+
+/// Deterministic weights in expected-name order (LN gamma near 1), as float32
+/// or, for the GEMM matrices, bf16 (truncated bits are as good as any here).
+void write_model(const cuvit::VitConfig& config, const std::string& path, bool bf16_matrices) {
+    cuvit::WeightFileWriter writer;
+    std::uint32_t state = 12345U;
+    auto next = [&state] {
+        state = state * 1664525U + 1013904223U;
+        return (static_cast<float>(state >> 8) / 16777216.0F - 0.5F) * 0.4F;
+    };
+    const cuvit::Extent e = config.embed_dim;
+    const cuvit::Extent t = config.token_count();
+    const cuvit::Extent h = config.mlp_hidden;
+    const cuvit::Extent c = config.classes;
+    for (const std::string& name : cuvit::VisionTransformer::expected_tensor_names(config)) {
+        std::vector<Extent> shape;
+        const bool matrix = name.find("qkv.weight") != std::string::npos ||
+                            name.find("proj.weight") != std::string::npos ||
+                            name.find("fc1.weight") != std::string::npos ||
+                            name.find("fc2.weight") != std::string::npos || name == "head.weight";
+        if (name == "cls_token") shape = {1, 1, e};
+        else if (name == "pos_embed") shape = {1, t, e};
+        else if (name == "patch_embed.proj.weight")
+            shape = {e, config.channels, config.patch_size, config.patch_size};
+        else if (name.find("qkv.weight") != std::string::npos) shape = {3 * e, e};
+        else if (name.find("qkv.bias") != std::string::npos) shape = {3 * e};
+        else if (name.find("fc1.weight") != std::string::npos) shape = {h, e};
+        else if (name.find("fc1.bias") != std::string::npos) shape = {h};
+        else if (name.find("fc2.weight") != std::string::npos) shape = {e, h};
+        else if (name.find("proj.weight") != std::string::npos) shape = {e, e};
+        else if (name == "head.weight") shape = {c, e};
+        else if (name == "head.bias") shape = {c};
+        else shape = {e}; // biases of width e, LN gamma and beta
+        Extent count = 1;
+        for (const Extent x : shape) count *= x;
+        const bool gamma = name.find("norm") != std::string::npos &&
+                           name.find("weight") != std::string::npos;
+        std::vector<float> values(static_cast<std::size_t>(count));
+        for (float& v : values) v = (gamma ? 1.0F : 0.0F) + next();
+        if (bf16_matrices && matrix) { // "proj.weight" covers patch_embed.proj.weight
+            std::vector<std::uint16_t> bits(values.size());
+            for (std::size_t i = 0; i < values.size(); ++i) {
+                std::uint32_t word = 0;
+                std::memcpy(&word, &values[i], sizeof(word));
+                bits[i] = static_cast<std::uint16_t>(word >> 16);
+            }
+            writer.add_bf16(name, shape, bits.data());
+        } else {
+            writer.add(name, shape, values.data());
+        }
+    }
+    writer.write(path);
+}
+
+void model_through_the_cpp_api() {
+    const cuvit::VitConfig config = small_config();
+    write_model(config, "model.cvw", false);
+    write_model(config, "model_bf16.cvw", true);
+    const cuvit::WeightFile file = cuvit::WeightFile::load("model.cvw");
+    const cuvit::WeightFile file_bf16 = cuvit::WeightFile::load("model_bf16.cvw");
+    require(file.version() == 1 && file_bf16.version() == 2, "weight file versions");
+
+    const std::size_t per_image = static_cast<std::size_t>(config.channels) * config.image_size *
+                                  config.image_size;
+    std::vector<float> images(3 * per_image);
+    for (std::size_t i = 0; i < images.size(); ++i) {
+        images[i] = std::sin(0.37F * static_cast<float>(i));
+    }
+    const std::vector<float> first(images.begin(), images.begin() + static_cast<long>(per_image));
+
+    for (const cuvit::Precision precision : {cuvit::Precision::kFloat32, cuvit::Precision::kBFloat16}) {
+        cuvit::VisionTransformer model(config, file, 3, precision);
+        require(model.precision() == precision, "precision is kept");
+        const std::vector<float> batch = model.forward(images);
+        const std::vector<float> alone = model.forward(first);
+        require(batch.size() == 3 * static_cast<std::size_t>(config.classes), "logit count");
+        for (const float v : batch) {
+            require(std::isfinite(v), "finite logits");
+        }
+        require(std::memcmp(batch.data(), alone.data(), alone.size() * sizeof(float)) == 0,
+                "an image in a batch equals the image alone (bitwise)");
+        require_throws<std::invalid_argument>(
+            [&] { (void)model.forward(std::vector<float>(4 * per_image)); }, "batch above max_batch");
+        require_throws<std::invalid_argument>(
+            [&] { (void)model.forward(std::vector<float>(per_image + 1)); }, "partial image");
+    }
+
+    // bf16 weights: loaded into either precision they match the float32 file
+    // holding the same (widened) values, bitwise.
+    cuvit::VisionTransformer from_bf16(config, file_bf16, 3, cuvit::Precision::kBFloat16);
+    const std::vector<float> reduced = from_bf16.forward(images);
+    cuvit::VisionTransformer fp32_of_bf16(config, file_bf16, 3);
+    const std::vector<float> widened = fp32_of_bf16.forward(images);
+    cuvit::VisionTransformer reference_fp32(config, file, 3);
+    const std::vector<float> full = reference_fp32.forward(images);
+    double diff = 0.0;
+    double norm = 0.0;
+    for (std::size_t i = 0; i < full.size(); ++i) {
+        diff += (static_cast<double>(reduced[i]) - full[i]) * (static_cast<double>(reduced[i]) - full[i]);
+        diff += (static_cast<double>(widened[i]) - full[i]) * (static_cast<double>(widened[i]) - full[i]);
+        norm += 2.0 * static_cast<double>(full[i]) * full[i];
+    }
+    require(std::sqrt(diff / norm) < 5.0e-2, "bf16 weights stay within bf16 error of float32");
+    std::remove("model.cvw");
+    std::remove("model_bf16.cvw");
+}
+
 int run(const std::vector<std::pair<std::string, std::function<void()>>>& cases) {
     int failures = 0;
     for (const auto& [name, body] : cases) {
@@ -435,7 +557,8 @@ int main(int argc, char** argv) {
         const int status = run({{"device_buffer_copies_and_bounds", device_buffer_copies_and_bounds},
                                 {"host_buffer_is_pinned_and_usable", host_buffer_is_pinned_and_usable},
                                 {"stream_pipeline", stream_pipeline},
-                                {"arena_carving", arena_carving}});
+                                {"arena_carving", arena_carving},
+                                {"model_through_the_cpp_api", model_through_the_cpp_api}});
         // A kernel that faulted asynchronously would surface here.
         const hipError_t sync = hipDeviceSynchronize();
         if (sync != hipSuccess) {
