@@ -22,6 +22,8 @@ copy ceiling a device-to-device copy of the same bytes over the same kind of
 vit_tiny_forward  the full batch-32 forward (89 launches: attention fused, positional add in the embedding GEMM) as one HIP graph.
 vit_*_forward_bf16 the bf16 model: ViT-Tiny at batch 32 and ViT-Base at batch 64.
 vit_base_b64_bf16 the bf16 twins at ViT-Base/16 batch-64 shapes, cold.
+size_sweep   LN, softmax and the gather at ViT-Tiny shapes for batches 32-1024,
+             each beside a same-bytes copy.
 cpu_baseline the CPU oracle (a restatement of the reference's CPU loops) on a
              bounded sample of the same workload, one core.
 
@@ -375,6 +377,54 @@ def vit_base_bf16_counters(torch, cuvit, flush):
         print(f"{name}: 3 cold launches", flush=True)
 
 
+SWEEP_BATCHES = (32, 128, 512, 1024)
+
+
+def size_sweep(torch, cuvit, device):
+    """The three path kernels at ViT-Tiny shapes for growing batches, each over
+    rotating buffer sets totalling more than 640 MB (so each launch is cold),
+    with a same-bytes device copy beside it: how close each kernel gets to
+    8 TB/s once the transfer amortizes the fixed launch and memory latency."""
+    results = {}
+    for batch in SWEEP_BATCHES:
+        rows = batch * TOKENS
+        sm_rows = batch * HEADS * TOKENS
+        cases = {
+            "layer_norm": (rows * EMBED * 2 * F32 + 2 * EMBED * F32, rows * EMBED),
+            "softmax": (sm_rows * TOKENS * 2 * F32, sm_rows * TOKENS),
+            "extract_patches": (batch * CHANNELS * IMAGE * IMAGE * 2 * F32,
+                                batch * CHANNELS * IMAGE * IMAGE),
+        }
+        entry = {}
+        for name, (nbytes, count) in cases.items():
+            sets = max(2, min(64, -(-POOL_BYTES // nbytes)))
+            x = [torch.randn(count, device=device) for _ in range(sets)]
+            y = [torch.empty(count, device=device) for _ in range(sets)]
+            gamma = torch.ones(EMBED, device=device)
+            beta = torch.zeros(EMBED, device=device)
+            launch = {
+                "layer_norm": lambda i: cuvit.layer_norm(x[i], gamma, beta, y[i], rows, EMBED, 1e-6),
+                "softmax": lambda i: cuvit.softmax(x[i], x[i], sm_rows, TOKENS),
+                "extract_patches": lambda i: cuvit.extract_patches(x[i], y[i], batch, CHANNELS,
+                                                                   IMAGE, IMAGE, PATCH),
+            }[name]
+            repeats = max(1, 64 // sets)
+            ms = timed_graph(torch, lambda: [launch(i) for i in range(sets)], repeats) / sets
+            half = nbytes // 2 // 16 * 16
+            src = [torch.empty(half, dtype=torch.uint8, device=device) for _ in range(sets)]
+            dst = [torch.empty(half, dtype=torch.uint8, device=device) for _ in range(sets)]
+            copy_ms = timed_graph(torch, lambda: [dst[i].copy_(src[i]) for i in range(sets)],
+                                  repeats) / sets
+            gbps = nbytes / (ms * 1e-3) / 1e9
+            entry[name] = {"us": round(ms * 1e3, 2), "GBps": round(gbps, 1),
+                           "frac_of_peak": round(gbps / HBM_PEAK_GBS, 4),
+                           "frac_of_copy": round(copy_ms / ms, 3), "MB": round(nbytes / 1e6, 1)}
+            del x, y, src, dst
+        results[f"b{batch}"] = entry
+    torch.cuda.empty_cache()
+    return results
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -470,6 +520,7 @@ def main():
                     "fused (bitwise equal to the bf16 GEMM -> softmax -> GEMM launches); MFMA bf16 "
                     "dense peak 2.5 PFLOP/s"}
     line["vit_base_b64_bf16"] = vit_base_bf16(torch, cuvit, device)
+    line["size_sweep"] = size_sweep(torch, cuvit, device)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)
