@@ -316,3 +316,29 @@ def test_gemm_bf16_rounds_like_the_oracle(cuvit, oracle, device, m, n, k, gelu, 
     oracle.gemm_problem_run(a, b, bias, expected, m=m, n=n, k=k, layout=1, accumulate=accumulate,
                             gelu=gelu)
     require_rounded(oracle, bf16_bits(out), expected, f"bf16 GEMM {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("k", [192, 520, 768, 1000, 3072])
+@pytest.mark.parametrize("gelu,accumulate", [(0, 0), (1, 0), (0, 1)])
+def test_gemm_bf16_rows_do_not_depend_on_the_tile(cuvit, oracle, device, k, gelu, accumulate):
+    """The same rows inside a tall problem (128 x 128 tile, 32- or 64-deep
+    stages by K) and alone (64 x 64 tile, 32- or 64-deep by K) are bitwise
+    equal: every bf16 tile walks K over the same k-blocks."""
+    m, n = 11008, 768  # 86 x 6 tiles of 128: past the 128 x 128 threshold (two per CU)
+    a_bits, _ = bf16_inputs(oracle, 9300 + k, m * k)
+    b_bits, _ = bf16_inputs(oracle, 9301 + k, n * k, 0.0, 0.05)
+    c_bits, _ = bf16_inputs(oracle, 9302, m * n)
+    bias = to_device(oracle.generator(9303).normal(n, 0.0, 0.02), device)
+    w = bf16_tensor(b_bits, device)
+    p = cuvit.gemm_problem(m, n, k, cuvit.TRANSPOSED)
+    p.epilogue.gelu, p.epilogue.accumulate = gelu, accumulate
+    tall = bf16_tensor(c_bits, device)
+    cuvit.gemm(bf16_tensor(a_bits, device), w, bias, tall, p)
+    full = bf16_bits(tall).reshape(m, n)
+    for start, rows in ((0, 197), (1000, 5), (m - 1, 1)):
+        q = cuvit.gemm_problem(rows, n, k, cuvit.TRANSPOSED)
+        q.epilogue.gelu, q.epilogue.accumulate = gelu, accumulate
+        piece = bf16_tensor(c_bits[start * n:(start + rows) * n], device)
+        cuvit.gemm(bf16_tensor(a_bits[start * k:(start + rows) * k], device), w, bias, piece, q)
+        require_exact(bf16_bits(piece).reshape(rows, n), full[start:start + rows],
+                      f"bf16 rows {start}..{start + rows} (K {k}) changed with the problem height")
