@@ -36,8 +36,9 @@
 // [images, tokens, heads, 64], bf16. A workgroup owns one (image, head) and
 // `waves` query tiles of 32 rows, one per wavefront. V of the (image, head)
 // sits in LDS transposed, [64][keys + 8], so a lane's weights.V B fragment is
-// 16 contiguous bytes and 16 consecutive rows hit distinct bank quads; Q and
-// K fragments are read straight from global memory (16 contiguous bytes).
+// 16 contiguous bytes, and K as [keys][64 + 8]; with the padding, 16
+// consecutive rows hit distinct bank quads. Q fragments are read straight
+// from global memory (16 contiguous bytes).
 #include "device_common.hpp"
 #include "gemm_kernel.hpp"
 #include "launch.hpp"
@@ -65,9 +66,14 @@ constexpr int kWavesPerGroup = 4;
 
 /// Elements per LDS row of transposed V for @p key_tiles 32-key tiles.
 __host__ __device__ constexpr int row_pitch(int key_tiles) { return key_tiles * kEdge + 8; }
+/// Elements per LDS row of K ([key][head_dim + 8]).
+constexpr int kKeyPitch = kHeadDim + 8;
 
+/// Transposed V, then K.
 __host__ __device__ constexpr std::size_t lds_bytes(int key_tiles) {
-    return static_cast<std::size_t>(kHeadDim) * row_pitch(key_tiles) * 2;
+    return (static_cast<std::size_t>(kHeadDim) * row_pitch(key_tiles) +
+            static_cast<std::size_t>(key_tiles) * kEdge * kKeyPitch) *
+           2;
 }
 
 /// 16 bytes at @p element of @p base, or zero when @p inside is false.
@@ -95,6 +101,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
     constexpr int kPitch = row_pitch(KT);
     extern __shared__ Vec16 lds_vectors[];
     std::uint16_t* const values = reinterpret_cast<std::uint16_t*>(lds_vectors); // [64][kPitch]
+    std::uint16_t* const keys = values + kHeadDim * kPitch;                      // [kPadded][72]
     const int waves = static_cast<int>(blockDim.x) / kWave;
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     const int lane = lane_id();
@@ -112,16 +119,19 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
     const std::uint16_t* const k_base = q_base + embed;
     const std::uint16_t* const v_base = q_base + 2 * embed;
 
-    // V transposed into LDS; keys past the tokens are zero.
+    // V transposed and K as is into LDS, shared by the workgroup's query
+    // tiles; keys past the tokens are zero.
     constexpr int kChunks = kHeadDim / 8;
     for (int c = threadIdx.x; c < kPadded * kChunks; c += blockDim.x) {
         const int key = c / kChunks;
         const int d0 = 8 * (c % kChunks);
         const Vec16 v = load_or_zero(v_base, key * qkv_row + d0, key < tokens);
+        const Vec16 k = load_or_zero(k_base, key * qkv_row + d0, key < tokens);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             Elem<std::uint16_t>::store_bits(values + (d0 + e) * kPitch + key, v, e);
         }
+        store16(keys + key * kKeyPitch + d0, k);
     }
     __syncthreads();
     const int query0 = (static_cast<int>(blockIdx.x) * waves + wave) * kEdge;
@@ -147,7 +157,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
         }
 #pragma unroll
         for (int kb = 0; kb < kHeadDim / kKBlock; ++kb) {
-            const Vec16 k = load_or_zero(k_base, key * qkv_row + kb * kKBlock + chunk, key < tokens);
+            const Vec16 k = load16(keys + key * kKeyPitch + kb * kKBlock + chunk);
             Bf16Mma::run(x[kt], k, q[kb]);
         }
     }
@@ -270,13 +280,22 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
 template <int KT>
 hipError_t launch(const std::uint16_t* qkv, std::uint16_t* context, int images, int heads,
                   int tokens, hipStream_t stream) {
-    // Four query tiles per workgroup: measured against 1, 2, 3 and 7 on
-    // MI355X, it was fastest or within 3% at 197 tokens for 12 to 768
-    // (image, head) pairs (ViT-Tiny b32: 13.1 us against 18.7 with all seven
-    // tiles in one workgroup; ViT-Base b64: 56.7 against 55.2).
+    // Query tiles per workgroup, measured on MI355X at 197 tokens: all of
+    // them (one K/V load per (image, head)) once there are two (image, head)
+    // pairs per compute unit (ViT-Base b64: 47.1 us against 49.9 with four),
+    // four below that (ViT-Tiny b32: 11.4 us against 14.8 with seven).
     const int query_tiles = (tokens + kEdge - 1) / kEdge;
     const std::int64_t pairs = static_cast<std::int64_t>(images) * heads;
-    const int waves = query_tiles < kWavesPerGroup ? query_tiles : kWavesPerGroup;
+    const int per_group = pairs >= 2 * static_cast<std::int64_t>(compute_units()) ? kMaxWaves
+                                                                                  : kWavesPerGroup;
+    const int waves = query_tiles < per_group ? query_tiles : per_group;
+    // Above 64 KiB (256 tokens) the kernel opts in to more LDS, once per device.
+    static std::atomic<std::uint64_t> opted_in{0};
+    if (const hipError_t opted = allow_lds(reinterpret_cast<const void*>(attention_bf16_kernel<KT>),
+                                           lds_bytes(KT), opted_in);
+        opted != hipSuccess) {
+        return opted;
+    }
     const dim3 grid(static_cast<unsigned int>((query_tiles + waves - 1) / waves),
                     static_cast<unsigned int>(pairs));
     const float scale = 1.0F / std::sqrt(static_cast<float>(kHeadDim));
