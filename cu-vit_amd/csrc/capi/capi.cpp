@@ -268,6 +268,31 @@ int gemm_bf16_with_addend(const std::uint16_t* a, const std::uint16_t* b, const 
     return from_hip(detail::gemm_bf16(a, b, bias, c, resolved.args, stream), "gemm launch");
 }
 
+int layer_norm_cached(const float* input, const float* gamma, const float* beta, float* output,
+                      int rows, int columns, float epsilon, hipStream_t stream) {
+    bool empty = false;
+    if (const int s = check_layer_norm(input, gamma, beta, output, rows, columns, &empty);
+        s != CUVIT_OK || empty) {
+        return s;
+    }
+    return from_hip(detail::layer_norm_f32(input, gamma, beta, output, rows, columns, epsilon,
+                                           stream, false),
+                    "layer_norm launch");
+}
+
+int layer_norm_cached(const std::uint16_t* input, const float* gamma, const float* beta,
+                      std::uint16_t* output, int rows, int columns, float epsilon,
+                      hipStream_t stream) {
+    bool empty = false;
+    if (const int s = check_layer_norm(input, gamma, beta, output, rows, columns, &empty);
+        s != CUVIT_OK || empty) {
+        return s;
+    }
+    return from_hip(detail::layer_norm_bf16(input, gamma, beta, output, rows, columns, epsilon,
+                                            stream, false),
+                    "layer_norm launch");
+}
+
 } // namespace cuvit::capi
 
 using namespace cuvit;

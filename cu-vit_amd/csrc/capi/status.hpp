@@ -40,6 +40,16 @@ int gemm_bf16_with_addend(const std::uint16_t* a, const std::uint16_t* b, const 
                           const float* addend, int ld_addend, std::uint16_t* c,
                           const cuvit_gemm_problem* problem, hipStream_t stream);
 
+/// cuvit_layer_norm_f32 / _bf16 with plain (cached) output stores, for a
+/// caller whose next launch reads the output: the model's blocks, where the
+/// normalised rows feed a GEMM at once. Same validation and values as the C
+/// ABI's entry points, which store non-temporally.
+int layer_norm_cached(const float* input, const float* gamma, const float* beta, float* output,
+                      int rows, int columns, float epsilon, hipStream_t stream);
+int layer_norm_cached(const std::uint16_t* input, const float* gamma, const float* beta,
+                      std::uint16_t* output, int rows, int columns, float epsilon,
+                      hipStream_t stream);
+
 /// Runs @p body, mapping any exception it throws to the matching status.
 template <typename Body> int guarded(Body&& body) {
     try {

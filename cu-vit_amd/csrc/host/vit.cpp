@@ -12,7 +12,9 @@
 // into rows 1.. of each image -> class token into row 0 -> positional add ->
 // blocks -> final LN -> head GEMM on the class rows only. Here the positional
 // add rides in the embedding GEMM's epilogue and row 0 is one broadcast of
-// cls + pos[0], with the same bits as the separate launches.
+// cls + pos[0], with the same bits as the separate launches. The model's
+// LayerNorms store their rows with plain (cached) stores, since a GEMM reads
+// them next; the C ABI's LayerNorm stores non-temporally. Same values.
 #include "cuvit/vit.hpp"
 
 #include "cuvit/capi.h"
@@ -401,8 +403,9 @@ void VisionTransformer::run_block(const BlockWeights& block,
     const int qkv_row = 3 * embed;
     T* const tokens = stored.tokens;
 
-    launch_layer_norm(tokens, block.norm1_gamma, block.norm1_beta, stored.normalized, rows, embed,
-                      config_.layer_norm_epsilon, stream);
+    throw_on_error(capi::layer_norm_cached(tokens, block.norm1_gamma, block.norm1_beta,
+                                           stored.normalized, rows, embed,
+                                           config_.layer_norm_epsilon, stream));
 
     // [tokens, 3, heads, head_dim] in one projection.
     launch_gemm(stored.normalized, matrices.qkv, block.qkv_bias, stored.qkv,
@@ -426,8 +429,9 @@ void VisionTransformer::run_block(const BlockWeights& block,
     projection.epilogue.accumulate = true;
     launch_gemm(stored.context, matrices.proj, block.proj_bias, tokens, projection, stream);
 
-    launch_layer_norm(tokens, block.norm2_gamma, block.norm2_beta, stored.normalized, rows, embed,
-                      config_.layer_norm_epsilon, stream);
+    throw_on_error(capi::layer_norm_cached(tokens, block.norm2_gamma, block.norm2_beta,
+                                           stored.normalized, rows, embed,
+                                           config_.layer_norm_epsilon, stream));
 
     GemmProblem fc1 = gemm_problem(rows, hidden, embed, GemmLayout::kTransposed);
     fc1.epilogue.gelu = true;
@@ -493,8 +497,9 @@ void VisionTransformer::forward_stored(Stored<T>& stored, const float* images, f
         run_block<T>(blocks_[index], stored.blocks[index], stored, batch, stream);
     }
 
-    launch_layer_norm(stored.tokens, final_gamma_, final_beta_, stored.normalized,
-                      batch * token_count, embed, config_.layer_norm_epsilon, stream);
+    throw_on_error(capi::layer_norm_cached(stored.tokens, final_gamma_, final_beta_,
+                                           stored.normalized, batch * token_count, embed,
+                                           config_.layer_norm_epsilon, stream));
 
     // Class-token pooling: one row per image feeds the head.
     GemmProblem head = gemm_problem(1, config_.classes, embed, GemmLayout::kTransposed);

@@ -11,12 +11,15 @@
 
 namespace cuvit::detail {
 
-// layer_norm.hip
+// layer_norm.hip. With @p streaming the output is stored non-temporally
+// (best when it is read back from HBM later); without, it stays in the
+// caches for a kernel that reads it next. The values are the same.
 hipError_t layer_norm_f32(const float* input, const float* gamma, const float* beta, float* output,
-                          int rows, int columns, float epsilon, hipStream_t stream);
+                          int rows, int columns, float epsilon, hipStream_t stream,
+                          bool streaming = true);
 hipError_t layer_norm_bf16(const std::uint16_t* input, const float* gamma, const float* beta,
                            std::uint16_t* output, int rows, int columns, float epsilon,
-                           hipStream_t stream);
+                           hipStream_t stream, bool streaming = true);
 
 // softmax.hip
 hipError_t softmax_f32(const float* input, float* output, int rows, int columns,

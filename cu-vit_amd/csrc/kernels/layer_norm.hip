@@ -43,7 +43,10 @@ __device__ __forceinline__ float lane_broadcast(float v, int source_lane) {
     return __int_as_float(__builtin_amdgcn_ds_bpermute(source_lane << 2, __float_as_int(v)));
 }
 
-template <typename T, int Lanes, int V>
+/// @tparam Streaming non-temporal output stores (for an output read later
+/// from HBM); plain ones leave it in the caches for a kernel that reads it
+/// next.
+template <typename T, int Lanes, int V, bool Streaming>
 __global__ __launch_bounds__(kBlock) void layer_norm_vector_kernel(
     const T* __restrict__ input, const float* __restrict__ gamma, const float* __restrict__ beta,
     T* __restrict__ output, int rows, int columns, float epsilon) {
@@ -167,7 +170,11 @@ __global__ __launch_bounds__(kBlock) void layer_norm_vector_kernel(
                             Elem<T>::set(result, e + i, d[j][e + i] * inverse_deviation * gv[i] + bv[i]);
                         }
                     }
-                    store16_streaming(destination + (team_lane + Lanes * j) * E, result);
+                    if constexpr (Streaming) {
+                        store16_streaming(destination + (team_lane + Lanes * j) * E, result);
+                    } else {
+                        store16(destination + (team_lane + Lanes * j) * E, result);
+                    }
                 }
             }
         }
@@ -216,42 +223,43 @@ constexpr int kWavesPerCu = 16;
 
 template <typename T, int Lanes, int V>
 hipError_t launch_vector(const T* input, const float* gamma, const float* beta, T* output, int rows,
-                         int columns, float epsilon, hipStream_t stream) {
+                         int columns, float epsilon, bool streaming, hipStream_t stream) {
     constexpr int kTeams = kWave / Lanes;
     const std::int64_t groups = (static_cast<std::int64_t>(rows) + kTeams - 1) / kTeams;
     const unsigned int grid = stride_grid(groups, kWavesPerBlock, kWavesPerCu / kWavesPerBlock);
-    layer_norm_vector_kernel<T, Lanes, V>
-        <<<grid, kBlock, 0, stream>>>(input, gamma, beta, output, rows, columns, epsilon);
+    auto kernel = streaming ? layer_norm_vector_kernel<T, Lanes, V, true>
+                            : layer_norm_vector_kernel<T, Lanes, V, false>;
+    kernel<<<grid, kBlock, 0, stream>>>(input, gamma, beta, output, rows, columns, epsilon);
     return hipGetLastError();
 }
 
 template <typename T>
 hipError_t dispatch(const T* input, const float* gamma, const float* beta, T* output, int rows,
-                    int columns, float epsilon, hipStream_t stream) {
+                    int columns, float epsilon, bool streaming, hipStream_t stream) {
     constexpr int E = Elem<T>::kPerVec;
     const bool vectorizable = columns % E == 0 && aligned16(input) && aligned16(output) &&
                               aligned16(gamma) && aligned16(beta);
     const int vectors = columns / E;
     if (vectorizable && vectors <= 16 * 8) {
         switch ((vectors + 15) / 16) {
-        case 1: return launch_vector<T, 16, 1>(input, gamma, beta, output, rows, columns, epsilon, stream);
-        case 2: return launch_vector<T, 16, 2>(input, gamma, beta, output, rows, columns, epsilon, stream);
-        case 3: return launch_vector<T, 16, 3>(input, gamma, beta, output, rows, columns, epsilon, stream);
-        case 4: return launch_vector<T, 16, 4>(input, gamma, beta, output, rows, columns, epsilon, stream);
-        case 5: return launch_vector<T, 16, 5>(input, gamma, beta, output, rows, columns, epsilon, stream);
-        case 6: return launch_vector<T, 16, 6>(input, gamma, beta, output, rows, columns, epsilon, stream);
-        case 7: return launch_vector<T, 16, 7>(input, gamma, beta, output, rows, columns, epsilon, stream);
-        default: return launch_vector<T, 16, 8>(input, gamma, beta, output, rows, columns, epsilon, stream);
+        case 1: return launch_vector<T, 16, 1>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
+        case 2: return launch_vector<T, 16, 2>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
+        case 3: return launch_vector<T, 16, 3>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
+        case 4: return launch_vector<T, 16, 4>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
+        case 5: return launch_vector<T, 16, 5>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
+        case 6: return launch_vector<T, 16, 6>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
+        case 7: return launch_vector<T, 16, 7>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
+        default: return launch_vector<T, 16, 8>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
         }
     }
     if (vectorizable && vectors <= kWave * 8) {
         switch ((vectors + kWave - 1) / kWave) {
-        case 3: return launch_vector<T, 64, 3>(input, gamma, beta, output, rows, columns, epsilon, stream);
-        case 4: return launch_vector<T, 64, 4>(input, gamma, beta, output, rows, columns, epsilon, stream);
-        case 5: return launch_vector<T, 64, 5>(input, gamma, beta, output, rows, columns, epsilon, stream);
-        case 6: return launch_vector<T, 64, 6>(input, gamma, beta, output, rows, columns, epsilon, stream);
-        case 7: return launch_vector<T, 64, 7>(input, gamma, beta, output, rows, columns, epsilon, stream);
-        default: return launch_vector<T, 64, 8>(input, gamma, beta, output, rows, columns, epsilon, stream);
+        case 3: return launch_vector<T, 64, 3>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
+        case 4: return launch_vector<T, 64, 4>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
+        case 5: return launch_vector<T, 64, 5>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
+        case 6: return launch_vector<T, 64, 6>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
+        case 7: return launch_vector<T, 64, 7>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
+        default: return launch_vector<T, 64, 8>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
         }
     }
     const unsigned int grid = stride_grid(rows, kWavesPerBlock, kWavesPerCu / kWavesPerBlock);
@@ -263,14 +271,15 @@ hipError_t dispatch(const T* input, const float* gamma, const float* beta, T* ou
 } // namespace
 
 hipError_t layer_norm_f32(const float* input, const float* gamma, const float* beta, float* output,
-                          int rows, int columns, float epsilon, hipStream_t stream) {
-    return dispatch<float>(input, gamma, beta, output, rows, columns, epsilon, stream);
+                          int rows, int columns, float epsilon, hipStream_t stream, bool streaming) {
+    return dispatch<float>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
 }
 
 hipError_t layer_norm_bf16(const std::uint16_t* input, const float* gamma, const float* beta,
                            std::uint16_t* output, int rows, int columns, float epsilon,
-                           hipStream_t stream) {
-    return dispatch<std::uint16_t>(input, gamma, beta, output, rows, columns, epsilon, stream);
+                           hipStream_t stream, bool streaming) {
+    return dispatch<std::uint16_t>(input, gamma, beta, output, rows, columns, epsilon, streaming,
+                                   stream);
 }
 
 } // namespace cuvit::detail
