@@ -6,6 +6,7 @@
 
 #include "../kernels/launch.hpp"
 
+#include <cmath>
 #include <cstdint>
 #include <string>
 
@@ -213,6 +214,57 @@ int check_gemm(const void* a, const void* b, const void* c, const cuvit_gemm_pro
     return ok();
 }
 
+/// Largest output side: size * size stays within a 32-bit pixel index.
+constexpr int kMaxPreprocessSize = 32768;
+
+/// check_preprocess_settings with the batch, the settings pointer and the
+/// operands around it.
+int check_preprocess(const void* pixels, int batch, int width, int height,
+                     const cuvit_preprocessing* settings, const void* tensor, bool* empty) {
+    *empty = batch == 0;
+    if (*empty) {
+        return ok();
+    }
+    if (batch < 0) {
+        return fail(CUVIT_ERROR_INVALID_ARGUMENT, "The preprocessing batch cannot be negative");
+    }
+    if (settings == nullptr) {
+        return fail(CUVIT_ERROR_INVALID_ARGUMENT, "Preprocessing settings cannot be null");
+    }
+    if (const int s = check_preprocess_settings(width, height, *settings); s != CUVIT_OK) {
+        return s;
+    }
+    if (pixels == nullptr || tensor == nullptr) {
+        return fail(CUVIT_ERROR_INVALID_ARGUMENT, "Preprocessing operands cannot be null");
+    }
+    if (settings->size > kMaxPreprocessSize) {
+        return fail(CUVIT_ERROR_LENGTH, "The preprocessing size exceeds the grid limit");
+    }
+    return ok();
+}
+
+/// Resize-and-crop geometry (image.cpp:113-121), each step rounded to float
+/// on its own: the shorter side goes to round(size / crop_fraction), the crop
+/// of size * scale source pixels is centred, and output pixels are step apart.
+detail::PreprocessGeometry preprocess_geometry(int width, int height,
+                                               const cuvit_preprocessing& settings) {
+#pragma clang fp contract(off)
+    const float size = static_cast<float>(settings.size);
+    const float resized = std::round(size / settings.crop_fraction);
+    const int shorter = width < height ? width : height;
+    const float scale = static_cast<float>(shorter) / resized;
+    const float crop = size * scale;
+    detail::PreprocessGeometry geometry{};
+    geometry.origin_x = (static_cast<float>(width) - crop) * 0.5F;
+    geometry.origin_y = (static_cast<float>(height) - crop) * 0.5F;
+    geometry.step = crop / size;
+    for (int channel = 0; channel < 3; ++channel) {
+        geometry.mean[channel] = settings.mean[channel];
+        geometry.stddev[channel] = settings.stddev[channel];
+    }
+    return geometry;
+}
+
 } // namespace
 
 int fail(cuvit_status status, const std::string& message) {
@@ -236,6 +288,25 @@ int from_hip(hipError_t result, const char* what) {
                                                  hipGetErrorString(result) + ')');
     last_hip = static_cast<int>(result);
     return status;
+}
+
+int check_preprocess_settings(int width, int height, const cuvit_preprocessing& settings) {
+    if (width <= 0 || height <= 0) {
+        return fail(CUVIT_ERROR_INVALID_ARGUMENT, "Cannot preprocess an empty image");
+    }
+    if (settings.size <= 0) {
+        return fail(CUVIT_ERROR_INVALID_ARGUMENT, "The preprocessing size must be positive");
+    }
+    if (!(settings.crop_fraction > 0.0F) || settings.crop_fraction > 1.0F) {
+        return fail(CUVIT_ERROR_INVALID_ARGUMENT, "The crop fraction must lie in (0, 1]");
+    }
+    for (const float deviation : settings.stddev) {
+        if (deviation == 0.0F) {
+            return fail(CUVIT_ERROR_INVALID_ARGUMENT,
+                        "A preprocessing standard deviation cannot be zero");
+        }
+    }
+    return ok();
 }
 
 int gemm_f32_with_addend(const float* a, const float* b, const float* bias, const float* addend,
@@ -408,6 +479,32 @@ int cuvit_extract_patches_bf16(const cuvit_bf16* images, cuvit_bf16* patches, in
     return from_hip(detail::extract_patches(images, patches, 2, batch, channels, height, width,
                                             patch, capi::as_hip(stream)),
                     "extract_patches launch");
+}
+
+void cuvit_preprocessing_default(cuvit_preprocessing* settings) {
+    if (settings == nullptr) {
+        return;
+    }
+    settings->size = 224;
+    settings->crop_fraction = 0.9F;
+    for (int channel = 0; channel < 3; ++channel) {
+        settings->mean[channel] = 0.5F;
+        settings->stddev[channel] = 0.5F;
+    }
+}
+
+int cuvit_preprocess_u8(const uint8_t* pixels, int batch, int width, int height,
+                        const cuvit_preprocessing* settings, float* tensor,
+                        cuvit_stream_t stream) {
+    bool empty = false;
+    if (const int s = capi::check_preprocess(pixels, batch, width, height, settings, tensor, &empty);
+        s != CUVIT_OK || empty) {
+        return s;
+    }
+    const detail::PreprocessGeometry geometry = capi::preprocess_geometry(width, height, *settings);
+    return from_hip(detail::preprocess_u8(pixels, batch, width, height, tensor, settings->size,
+                                          geometry, capi::as_hip(stream)),
+                    "preprocess launch");
 }
 
 int cuvit_add_f32(float* accumulator, const float* addend, int64_t count, cuvit_stream_t stream) {

@@ -1,6 +1,8 @@
-// C ABI of the host-side classes: weight files (cuvit/weights.hpp) and the
-// model driver (cuvit/vit.hpp). Exceptions become status codes here.
+// C ABI of the host-side classes: weight files (cuvit/weights.hpp), the
+// model driver (cuvit/vit.hpp) and PPM images (cuvit/image.hpp). Exceptions
+// become status codes here.
 #include "cuvit/capi.h"
+#include "cuvit/image.hpp"
 #include "cuvit/vit.hpp"
 #include "cuvit/weights.hpp"
 #include "status.hpp"
@@ -15,6 +17,10 @@ struct cuvit_weight_writer {
 
 struct cuvit_weight_file {
     cuvit::WeightFile file;
+};
+
+struct cuvit_image {
+    cuvit::RgbImage image;
 };
 
 struct cuvit_vit {
@@ -232,5 +238,29 @@ uint64_t cuvit_vit_activation_bytes(const cuvit_vit* model) {
 }
 
 void cuvit_vit_destroy(cuvit_vit* model) { delete model; }
+
+int cuvit_image_load_ppm(const char* path, cuvit_image** image) {
+    return guarded([&]() -> int {
+        if (path == nullptr || image == nullptr) {
+            return fail(CUVIT_ERROR_INVALID_ARGUMENT, "path and out-pointer cannot be null");
+        }
+        auto loaded = std::make_unique<cuvit_image>();
+        loaded->image = cuvit::load_ppm(path);
+        *image = loaded.release();
+        return CUVIT_OK;
+    });
+}
+
+int cuvit_image_width(const cuvit_image* image) { return image == nullptr ? 0 : image->image.width; }
+
+int cuvit_image_height(const cuvit_image* image) {
+    return image == nullptr ? 0 : image->image.height;
+}
+
+const uint8_t* cuvit_image_pixels(const cuvit_image* image) {
+    return image == nullptr ? nullptr : image->image.pixels.data();
+}
+
+void cuvit_image_destroy(cuvit_image* image) { delete image; }
 
 } // extern "C"

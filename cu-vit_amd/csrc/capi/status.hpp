@@ -50,6 +50,11 @@ int layer_norm_cached(const std::uint16_t* input, const float* gamma, const floa
                       std::uint16_t* output, int rows, int columns, float epsilon,
                       hipStream_t stream);
 
+/// The checks of preprocess (image.cpp:96-104, 126-128), in its order: an
+/// empty image, a non-positive size, a crop fraction outside (0, 1], a zero
+/// standard deviation.
+int check_preprocess_settings(int width, int height, const cuvit_preprocessing& settings);
+
 /// Runs @p body, mapping any exception it throws to the matching status.
 template <typename Body> int guarded(Body&& body) {
     try {

@@ -11,6 +11,19 @@
 
 namespace cuvit::detail {
 
+// preprocess.hip. The crop geometry of image.cpp:113-121, worked out on the
+// host, and the per-channel normalisation.
+struct PreprocessGeometry {
+    float origin_x;
+    float origin_y;
+    float step;
+    float mean[3];
+    float stddev[3];
+};
+hipError_t preprocess_u8(const std::uint8_t* pixels, int batch, int width, int height,
+                         float* tensor, int size, const PreprocessGeometry& geometry,
+                         hipStream_t stream);
+
 // layer_norm.hip. With @p streaming the output is stored non-temporally
 // (best when it is read back from HBM later); without, it stays in the
 // caches for a kernel that reads it next. The values are the same.

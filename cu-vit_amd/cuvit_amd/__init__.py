@@ -25,6 +25,7 @@ __all__ = [
     "broadcast", "convert_to_bf16", "convert_to_f32", "attention", "attention_supported",
     "gemm_problem", "WeightWriter", "WeightFile", "VisionTransformer",
     "NO_TRANSPOSE", "TRANSPOSED", "PRECISION_F32", "PRECISION_BF16",
+    "Preprocessing", "RgbImage", "load_ppm", "preprocess", "preprocess_image", "cli_path",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -137,6 +138,24 @@ class VitConfig(ctypes.Structure):
         return self.channels * self.patch_size * self.patch_size
 
 
+class Preprocessing(ctypes.Structure):
+    """cuvit_preprocessing / cuvit::Preprocessing (reference image.hpp:30-38),
+    with the reference's defaults: size 224, crop fraction 0.9, mean and
+    stddev 0.5 per channel."""
+
+    _fields_ = [
+        ("size", ctypes.c_int),
+        ("crop_fraction", ctypes.c_float),
+        ("mean", ctypes.c_float * 3),
+        ("stddev", ctypes.c_float * 3),
+    ]
+
+    def __init__(self, size: int = 224, crop_fraction: float = 0.9,
+                 mean=(0.5, 0.5, 0.5), stddev=(0.5, 0.5, 0.5)):
+        super().__init__(size, crop_fraction, (ctypes.c_float * 3)(*mean),
+                         (ctypes.c_float * 3)(*stddev))
+
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _L = ctypes.c_int64
@@ -189,6 +208,13 @@ _SIGNATURES = {
     "cuvit_vit_weight_bytes": (ctypes.c_uint64, [_P]),
     "cuvit_vit_activation_bytes": (ctypes.c_uint64, [_P]),
     "cuvit_vit_destroy": (None, [_P]),
+    "cuvit_image_load_ppm": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "cuvit_image_width": (_I, [_P]),
+    "cuvit_image_height": (_I, [_P]),
+    "cuvit_image_pixels": (_P, [_P]),
+    "cuvit_image_destroy": (None, [_P]),
+    "cuvit_preprocessing_default": (None, [ctypes.POINTER(Preprocessing)]),
+    "cuvit_preprocess_u8": (_I, [_P, _I, _I, _I, ctypes.POINTER(Preprocessing), _P, _P]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -505,3 +531,68 @@ def expected_tensor_names(config: VitConfig):
     names += [("norm.weight", (e,)), ("norm.bias", (e,)),
               ("head.weight", (config.classes, e)), ("head.bias", (config.classes,))]
     return names
+
+
+class RgbImage:
+    """cuvit::RgbImage (reference image.hpp:12-19): .pixels is a uint8 numpy
+    array of shape [height, width, 3], interleaved RGB."""
+
+    def __init__(self, width: int, height: int, pixels):
+        self.width = width
+        self.height = height
+        self.pixels = pixels
+
+    def empty(self) -> bool:
+        return self.pixels is None or self.pixels.size == 0
+
+
+def load_ppm(path: str) -> RgbImage:
+    """load_ppm (reference image.cpp:57-93) through the C ABI; a malformed or
+    missing file raises CuvitError with the reference's message."""
+    import numpy as np
+
+    lib = library()
+    handle = ctypes.c_void_p()
+    check(lib.cuvit_image_load_ppm(os.fsencode(path), ctypes.byref(handle)))
+    try:
+        width, height = lib.cuvit_image_width(handle), lib.cuvit_image_height(handle)
+        count = width * height * 3
+        buffer = (ctypes.c_uint8 * count).from_address(lib.cuvit_image_pixels(handle))
+        pixels = np.frombuffer(buffer, dtype=np.uint8).reshape(height, width, 3).copy()
+    finally:
+        lib.cuvit_image_destroy(handle)
+    return RgbImage(width, height, pixels)
+
+
+def preprocess(pixels, tensor, batch: int, width: int, height: int,
+               settings: Optional[Preprocessing] = None, stream=None) -> None:
+    """cuvit_preprocess_u8: @p batch device images [batch, height, width, 3]
+    uint8 into the device tensor [batch, 3, size, size] float (the reference's
+    preprocess, image.cpp:95-135, batched on the GPU)."""
+    settings = settings if settings is not None else Preprocessing()
+    check(library().cuvit_preprocess_u8(_ptr(pixels), batch, width, height,
+                                        ctypes.byref(settings), _ptr(tensor),
+                                        stream_handle(stream)))
+
+
+def preprocess_image(image: RgbImage, settings: Optional[Preprocessing] = None):
+    """The reference's preprocess(image, settings) -> [3, size, size] numpy
+    float32, computed on cuda:0 by the library's kernel."""
+    import numpy as np
+    import torch
+
+    settings = settings if settings is not None else Preprocessing()
+    if image.empty():
+        raise InvalidArgument(ERROR_INVALID_ARGUMENT, "Cannot preprocess an empty image")
+    device = torch.device("cuda:0")
+    pixels = torch.from_numpy(np.ascontiguousarray(image.pixels, dtype=np.uint8)).to(device)
+    size = settings.size
+    tensor = torch.empty(3 * max(size, 0) * max(size, 0), dtype=torch.float32, device=device)
+    preprocess(pixels, tensor, 1, image.width, image.height, settings)
+    torch.cuda.synchronize()
+    return tensor.cpu().numpy().reshape(3, size, size)
+
+
+def cli_path() -> str:
+    """The cu-vit command-line program built beside the library."""
+    return os.path.join(os.path.dirname(_HERE), "bin", "cu-vit")

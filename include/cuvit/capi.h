@@ -263,6 +263,44 @@ uint64_t cuvit_vit_weight_bytes(const cuvit_vit* model);
 uint64_t cuvit_vit_activation_bytes(const cuvit_vit* model);
 void cuvit_vit_destroy(cuvit_vit* model);
 
+/* ---------------------------------------------------------------------------
+ * Images (include/cuvit/image.hpp:10-52, src/runtime/image.cpp:57-135): binary
+ * PPM loading on the host and preprocessing on the device.
+ * ------------------------------------------------------------------------- */
+typedef struct cuvit_image cuvit_image;
+
+/* load_ppm(path) (image.cpp:57-93): a P6 file with maximum 255. Failures are
+ * CUVIT_ERROR_RUNTIME with the reference's messages. */
+int cuvit_image_load_ppm(const char* path, cuvit_image** image);
+/* Extents of a loaded image (0 for a null image). */
+int cuvit_image_width(const cuvit_image* image);
+int cuvit_image_height(const cuvit_image* image);
+/* width * height * 3 interleaved RGB bytes; valid while the image lives. */
+const uint8_t* cuvit_image_pixels(const cuvit_image* image);
+void cuvit_image_destroy(cuvit_image* image);
+
+/* Preprocessing (image.hpp:30-38). */
+typedef struct cuvit_preprocessing {
+    int size;
+    float crop_fraction;
+    float mean[3];
+    float stddev[3];
+} cuvit_preprocessing;
+
+/* Preprocessing{}: size 224, crop fraction 0.9, mean and stddev 0.5. */
+void cuvit_preprocessing_default(cuvit_preprocessing* settings);
+
+/* preprocess(image, settings) (image.cpp:95-135) on the device for @p batch
+ * images of one size: pixels [batch, height, width, 3] uint8, tensor
+ * [batch, 3, size, size] float, bit-identical to the reference's host loop.
+ * Validation: batch 0 returns at once; then a negative batch, a null settings
+ * pointer, the reference's four checks in its order (empty image, size,
+ * crop fraction, zero stddev), null operands (all CUVIT_ERROR_INVALID_ARGUMENT),
+ * and a size above 32768 (CUVIT_ERROR_LENGTH). The batch is an extension. */
+int cuvit_preprocess_u8(const uint8_t* pixels, int batch, int width, int height,
+                        const cuvit_preprocessing* settings, float* tensor,
+                        cuvit_stream_t stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

@@ -21,6 +21,13 @@
 //   generator - the mt19937_64 10000th-output value fixed by the C++ standard,
 //     committed first-values fixtures, distribution moments.
 //   round_bf16 - exhaustive properties on special values and ties.
+//   preprocess - bit-exact against the reference's src/runtime/image.cpp
+//     compiled into oracle/_ref; closed forms that fix it without the
+//     reference: identity geometry (a size x size image with crop fraction 1
+//     reproduces the normalised pixels), exact 2x2 box averages at a 2x
+//     downscale, transposing the image transposes the tensor, and the
+//     reference's own image_test cases (uniform grey, planar channels, centre
+//     crop, rejected settings).
 #include "oracle.h"
 
 #include <algorithm>
@@ -427,6 +434,60 @@ void oracle_round_bf16(const float* input, uint16_t* output, int64_t count) {
         const std::uint32_t lsb = (bits >> 16) & 1U;
         output[i] = static_cast<uint16_t>((bits + 0x7FFFU + lsb) >> 16);
     }
+}
+
+int oracle_preprocess(const uint8_t* pixels, int width, int height, int size, float crop_fraction,
+                      const float* mean, const float* stddev, float* tensor) {
+    // src/runtime/image.cpp:95-135, with the bilinear sample of 37-55 inline.
+    if (width <= 0 || height <= 0) {
+        return 1;
+    }
+    if (size <= 0) {
+        return 2;
+    }
+    if (!(crop_fraction > 0.0F) || crop_fraction > 1.0F) {
+        return 3;
+    }
+    for (int c = 0; c < 3; ++c) {
+        if (stddev[c] == 0.0F) {
+            return 4;
+        }
+    }
+    const float side = static_cast<float>(size);
+    const float target = std::round(side / crop_fraction);
+    const float scale = static_cast<float>(std::min(width, height)) / target;
+    const float window = side * scale;
+    const float x_origin = (static_cast<float>(width) - window) * 0.5F;
+    const float y_origin = (static_cast<float>(height) - window) * 0.5F;
+    const float step = window / side;
+
+    auto at = [&](int x, int y, int c) -> float {
+        const int cx = x < 0 ? 0 : (x >= width ? width - 1 : x);
+        const int cy = y < 0 ? 0 : (y >= height ? height - 1 : y);
+        return static_cast<float>(
+            pixels[(static_cast<std::size_t>(cy) * static_cast<std::size_t>(width) +
+                    static_cast<std::size_t>(cx)) * 3 + static_cast<std::size_t>(c)]);
+    };
+    const std::size_t plane = static_cast<std::size_t>(size) * static_cast<std::size_t>(size);
+    for (int c = 0; c < 3; ++c) {
+        for (int r = 0; r < size; ++r) {
+            const float y = y_origin + (static_cast<float>(r) + 0.5F) * step - 0.5F;
+            const int y0 = static_cast<int>(std::floor(y));
+            const float fy = y - static_cast<float>(y0);
+            for (int q = 0; q < size; ++q) {
+                const float x = x_origin + (static_cast<float>(q) + 0.5F) * step - 0.5F;
+                const int x0 = static_cast<int>(std::floor(x));
+                const float fx = x - static_cast<float>(x0);
+                const float upper = at(x0, y0, c) * (1.0F - fx) + at(x0 + 1, y0, c) * fx;
+                const float lower = at(x0, y0 + 1, c) * (1.0F - fx) + at(x0 + 1, y0 + 1, c) * fx;
+                const float sample = upper * (1.0F - fy) + lower * fy;
+                tensor[static_cast<std::size_t>(c) * plane +
+                       static_cast<std::size_t>(r) * static_cast<std::size_t>(size) +
+                       static_cast<std::size_t>(q)] = (sample / 255.0F - mean[c]) / stddev[c];
+            }
+        }
+    }
+    return 0;
 }
 
 } // extern "C"

@@ -72,6 +72,13 @@ void oracle_vit_forward_bf16(const oracle_vit_config* config, const float* const
 /* Round to bfloat16 bits, nearest-even (NaN kept quiet). */
 void oracle_round_bf16(const float* input, uint16_t* output, int64_t count);
 
+/* preprocess(image, settings) of src/runtime/image.cpp:95-135 for one
+ * interleaved RGB image: the [3, size, size] tensor. Returns 0, or the first
+ * failed check in the reference's order: 1 empty image, 2 size, 3 crop
+ * fraction, 4 zero stddev (then @p tensor is untouched). */
+int oracle_preprocess(const uint8_t* pixels, int width, int height, int size, float crop_fraction,
+                      const float* mean, const float* stddev, float* tensor);
+
 /* The reference tests' seeded DataGenerator (std::mt19937_64 with libstdc++'s
  * distributions, a fresh distribution object per fill call). */
 typedef struct oracle_generator oracle_generator;

@@ -144,6 +144,7 @@ class Oracle(_Linear):
             "oracle_generator_integers": (None, [_P, _P, _L, _L, _L]),
             "oracle_generator_raw": (ctypes.c_uint64, [_P]),
             "oracle_generator_destroy": (None, [_P]),
+            "oracle_preprocess": (_I, [_P, _I, _I, _I, _F, _P, _P, _P]),
         }
         for name, (res, args) in s.items():
             fn = getattr(self.lib, name)
@@ -165,6 +166,12 @@ class Oracle(_Linear):
         assert c.dtype == np.float32 and c.flags.c_contiguous
         self.lib.oracle_gemm_problem_run(_p(a), _p(b), _p(bias), _p(c), ctypes.byref(problem))
         return c
+
+    def preprocess(self, pixels, size: int = 224, crop_fraction: float = 0.9,
+                   mean=(0.5, 0.5, 0.5), stddev=(0.5, 0.5, 0.5)):
+        """[3, size, size] float32 of one [height, width, 3] uint8 image, or
+        the failed check's code (1 empty image, 2 size, 3 crop, 4 stddev)."""
+        return _preprocess(self.lib.oracle_preprocess, pixels, size, crop_fraction, mean, stddev)
 
     def extract_patches(self, images, batch, channels, height, width, patch) -> np.ndarray:
         images = _f32(images)
@@ -262,6 +269,8 @@ class Reference(_Linear):
                                        ctypes.POINTER(_I), ctypes.POINTER(_L), ctypes.POINTER(_P)]),
             "ref_weights_read": (_I, [ctypes.c_char_p, ctypes.c_char_p, _I, ctypes.POINTER(_L), _P, _L]),
             "ref_weights_check": (_I, [ctypes.c_char_p]),
+            "ref_preprocess": (_I, [_P, _I, _I, _I, _F, _P, _P, _P]),
+            "ref_load_ppm": (_I, [ctypes.c_char_p, ctypes.POINTER(_I), ctypes.POINTER(_I), _P, _L]),
         }
         for name, (res, args) in s.items():
             fn = getattr(self.lib, name)
@@ -296,11 +305,41 @@ class Reference(_Linear):
             raise RuntimeError(self.last_error())
         return out
 
+    def preprocess(self, pixels, size: int = 224, crop_fraction: float = 0.9,
+                   mean=(0.5, 0.5, 0.5), stddev=(0.5, 0.5, 0.5)):
+        """The reference's preprocess: [3, size, size] float32, or its error
+        message (a str) when it throws."""
+        out = _preprocess(self.lib.ref_preprocess, pixels, size, crop_fraction, mean, stddev)
+        return self.last_error() if isinstance(out, int) else out
+
+    def load_ppm(self, path: str):
+        """(width, height, [height, width, 3] uint8) from the reference's
+        load_ppm, or its error message (a str)."""
+        width, height = _I(), _I()
+        if self.lib.ref_load_ppm(os.fsencode(path), ctypes.byref(width), ctypes.byref(height),
+                                 None, 0):
+            return self.last_error()
+        pixels = np.empty((height.value, width.value, 3), dtype=np.uint8)
+        self.lib.ref_load_ppm(os.fsencode(path), ctypes.byref(width), ctypes.byref(height),
+                              _p(pixels), pixels.size)
+        return width.value, height.value, pixels
+
     def check_weights(self, path: str) -> Optional[str]:
         """None when the reference loads @p path, else its error message."""
         if self.lib.ref_weights_check(os.fsencode(path)):
             return self.last_error()
         return None
+
+
+def _preprocess(fn, pixels, size, crop_fraction, mean, stddev):
+    pixels = np.ascontiguousarray(pixels, dtype=np.uint8)
+    height, width = (pixels.shape[0], pixels.shape[1]) if pixels.ndim == 3 else (0, 0)
+    out = np.zeros((3, max(size, 0), max(size, 0)), dtype=np.float32)
+    m = (_F * 3)(*mean)
+    s = (_F * 3)(*stddev)
+    status = fn(_p(pixels) if pixels.size else None, width, height, size, crop_fraction,
+                ctypes.cast(m, _P), ctypes.cast(s, _P), _p(out))
+    return status if status else out
 
 
 def reference_available() -> bool:

@@ -2,9 +2,11 @@
 // /root/reference by oracle/Makefile into oracle/_ref/libref.so. TEST
 // INFRASTRUCTURE ONLY: it lets the tests check the oracle's restatement
 // bit-for-bit against the reference's tests/reference/linear_algebra.hpp and
-// elementwise.hpp, and the weight-file code against src/runtime/weights.cpp.
+// elementwise.hpp, the weight-file code against src/runtime/weights.cpp and
+// the image code against src/runtime/image.cpp.
 // Nothing here is a stand-in for reference code: every computation below is
 // a direct call into the reference's headers and sources.
+#include "cuvit/image.hpp"
 #include "cuvit/weights.hpp"
 #include "reference/elementwise.hpp"
 #include "reference/linear_algebra.hpp"
@@ -106,6 +108,50 @@ int ref_weights_read(const char* path, const char* name, int rank, const int64_t
 int ref_weights_check(const char* path) {
     try {
         static_cast<void>(cuvit::WeightFile::load(path));
+        return 0;
+    } catch (const std::exception& error) {
+        last_error = error.what();
+        return 1;
+    }
+}
+
+// preprocess() of src/runtime/image.cpp on one interleaved RGB image. Returns
+// 0, or 1 with the reference's message in ref_last_error().
+int ref_preprocess(const uint8_t* pixels, int width, int height, int size, float crop_fraction,
+                   const float* mean, const float* stddev, float* tensor) {
+    try {
+        cuvit::RgbImage image;
+        image.width = width;
+        image.height = height;
+        if (width > 0 && height > 0) {
+            image.pixels.assign(pixels, pixels + static_cast<std::size_t>(width) * height * 3);
+        }
+        cuvit::Preprocessing settings;
+        settings.size = size;
+        settings.crop_fraction = crop_fraction;
+        for (std::size_t c = 0; c < 3; ++c) {
+            settings.mean[c] = mean[c];
+            settings.stddev[c] = stddev[c];
+        }
+        const std::vector<float> out = cuvit::preprocess(image, settings);
+        std::memcpy(tensor, out.data(), out.size() * sizeof(float));
+        return 0;
+    } catch (const std::exception& error) {
+        last_error = error.what();
+        return 1;
+    }
+}
+
+// load_ppm() of src/runtime/image.cpp. Returns 0 with the extents and, when
+// @p capacity allows, the pixels; 1 with the reference's message otherwise.
+int ref_load_ppm(const char* path, int* width, int* height, uint8_t* pixels, int64_t capacity) {
+    try {
+        const cuvit::RgbImage image = cuvit::load_ppm(path);
+        *width = image.width;
+        *height = image.height;
+        if (static_cast<int64_t>(image.pixels.size()) <= capacity) {
+            std::memcpy(pixels, image.pixels.data(), image.pixels.size());
+        }
         return 0;
     } catch (const std::exception& error) {
         last_error = error.what();

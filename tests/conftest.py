@@ -40,6 +40,15 @@ def reference():
 
 
 @pytest.fixture(scope="session")
+def reference_or_none():
+    """The reference's CPU code where oracle/_ref is built, else None (for
+    tests whose extra reference check is optional)."""
+    from oracle import Reference, reference_available
+
+    return Reference() if reference_available() else None
+
+
+@pytest.fixture(scope="session")
 def lib():
     import cuvit_amd
 
