@@ -425,6 +425,31 @@ def size_sweep(torch, cuvit, device):
     return results
 
 
+def preprocess_block(torch, cuvit, device):
+    """The image front end: 32 RGB images of 320 x 240 (uint8, interleaved)
+    resampled, centre-cropped and normalised to [32, 3, 224, 224] fp32 in one
+    launch, cold (rotating pools > 512 MB). Algorithmic bytes: every pixel byte
+    read once plus every tensor value written once."""
+    batch, width, height, size = 32, 320, 240, 224
+    nbytes = batch * (width * height * 3 + 3 * size * size * 4)
+    sets = max(2, -(-POOL_BYTES // nbytes))
+    pixels = [torch.randint(0, 256, (batch * height * width * 3,), dtype=torch.uint8, device=device)
+              for _ in range(sets)]
+    tensors = [torch.empty(batch * 3 * size * size, device=device) for _ in range(sets)]
+    settings = cuvit.Preprocessing(size)
+    launch = lambda i: cuvit.preprocess(pixels[i], tensors[i], batch, width, height, settings)
+    ms = timed_graph(torch, lambda: [launch(i) for i in range(sets)], max(1, 200 // sets)) / sets
+    copy_ms = copy_ceiling(torch, device, nbytes)
+    del pixels, tensors
+    return {"workload": f"{batch} x {width}x{height} RGB u8 -> [{batch},3,{size},{size}] fp32",
+            "us_per_launch": round(ms * 1e3, 3), "bytes": nbytes,
+            "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_of_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "copy_us_same_bytes": round(copy_ms * 1e3, 3),
+            "frac_of_copy": round(copy_ms / ms, 3),
+            "images_per_s": round(batch / (ms * 1e-3), 1)}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -521,6 +546,7 @@ def main():
                     "dense peak 2.5 PFLOP/s"}
     line["vit_base_b64_bf16"] = vit_base_bf16(torch, cuvit, device)
     line["size_sweep"] = size_sweep(torch, cuvit, device)
+    line["preprocess"] = preprocess_block(torch, cuvit, device)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -52,8 +52,9 @@ def test_batch_of_distinct_images(cuvit, oracle, device):
 
 
 def test_batch_beyond_one_grid_dimension(cuvit, oracle, device):
-    """70,000 one-pixel images at size 2: more images than the grid's y
-    extent, so the kernel's image loop runs more than once per workgroup."""
+    """70,000 one-pixel images at size 2 (the one-pixel-per-thread kernel):
+    more images than the grid's y extent, so the kernel's image loop runs
+    more than once per workgroup."""
     batch = 70000
     images = np.random.default_rng(7).integers(0, 256, (batch, 1, 1, 3), dtype=np.uint8)
     settings = cuvit.Preprocessing(size=2, crop_fraction=1.0)
@@ -64,6 +65,30 @@ def test_batch_beyond_one_grid_dimension(cuvit, oracle, device):
     assert np.array_equal(bits(actual), bits(expected))
     for i in (0, 65534, 65535, 65536, batch - 1):
         assert np.array_equal(bits(actual[i]), bits(oracle.preprocess(images[i], 2, 1.0)))
+
+
+def test_batch_beyond_one_grid_dimension_four_columns(cuvit, oracle, device):
+    """The same on the four-column kernel: 70,000 images of 2 x 1 pixels at
+    size 4."""
+    batch = 70000
+    images = np.random.default_rng(8).integers(0, 256, (batch, 1, 2, 3), dtype=np.uint8)
+    settings = cuvit.Preprocessing(size=4, crop_fraction=1.0)
+    actual = run(cuvit, device, images, settings)
+    assert not np.isnan(actual).any()
+    for i in (0, 1, 65534, 65535, 65536, 65537, batch - 1):
+        assert np.array_equal(bits(actual[i]), bits(oracle.preprocess(images[i], 4, 1.0))), i
+
+
+def test_unaligned_tensor_takes_the_scalar_kernel(cuvit, oracle, device):
+    """A tensor 4 bytes past a 16-byte boundary cannot take 16-byte stores:
+    the one-pixel-per-thread kernel runs, with the same bits."""
+    pixels = random_pixels(13, 150, 170)
+    storage = torch.full((3 * 224 * 224 + 1,), float("nan"), device=device)
+    cuvit.preprocess(to_device(pixels[None], device), storage[1:], 1, 170, 150,
+                     cuvit.Preprocessing())
+    actual = to_host(storage)[1:].reshape(3, 224, 224)
+    assert np.isnan(to_host(storage)[0])
+    assert np.array_equal(bits(actual), bits(oracle.preprocess(pixels)))
 
 
 def test_side_stream(cuvit, oracle, device):
