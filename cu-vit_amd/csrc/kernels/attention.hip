@@ -11,13 +11,12 @@
 //     16 (MFMA s of a block sums k = kb + s, kb + 4 + s, kb + 8 + s,
 //     kb + 12 + s), then alpha * sum, exactly as in the GEMM epilogue;
 //   * softmax: the max is exact in any order; the exponentials are the same
-//     exp2((x - max) * log2 e); the sum reproduces the full-wavefront softmax
-//     (one 64-lane team per row): lane c' of that team sums the columns
-//     c' + 64 j in order from +0, then the DPP tree (quad swap 1, quad swap 2,
-//     half-row mirror, row mirror) and (r0 + r1) + (r2 + r3) over the four
-//     row totals. Here the same 64 partial sums sit in the registers of the
-//     four lanes that hold a query row, and the tree is replayed with two
-//     cross-lane exchanges; probabilities are e * (1 / sum) as there;
+//     exp2((x - max) * log2 e); the sum reproduces the softmax kernel's
+//     16-lane team (rows up to 256 wide): team lane t sums the columns
+//     t + 16 j in order from +0, then the DPP tree (pair, quad, half-row
+//     mirror, row mirror). Here the 16 partial sums sit four to a lane in
+//     the four lanes that hold a query row, and the tree is replayed with
+//     two cross-lane exchanges; probabilities are e * (1 / sum) as there;
 //   * weights.V: the GEMM's MFMA over keys in k-blocks of 16, keys past the
 //     token count contributing exact zeros.
 // The probabilities never leave registers: a lane of the logits tile holds
@@ -150,58 +149,25 @@ __global__ __launch_bounds__(Waves * kWave) void attention_kernel(const float* _
         }
     }
 
-    // The full-wavefront softmax's sum. Its lane c' = 16 a + 4 g + r sums
-    // columns c' + 64 j, j = 0..3: key tiles 4 j + a, element r of group g,
-    // all in this lane's registers.
-    float v[4][4];
+    // The softmax's sum (16-lane teams, softmax_terms.hpp): team lane t sums
+    // columns t + 16 j in order from +0, i.e. tile j, element t of the tile,
+    // which this lane holds for t = 4 g + r. Then the team's DPP tree:
+    // pairs (t ^ 1), quads (t ^ 2), quad 0 + quad 1 and quad 2 + quad 3 (the
+    // half-row mirror), and the two halves (the row mirror); here the quad
+    // totals sit in the four lanes of a query row, one exchange per level.
+    float partial[4];
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
+    for (int r = 0; r < 4; ++r) {
+        float sum = 0.F;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            float partial = 0.F;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                partial += s[4 * j + a][r];
-            }
-            v[a][r] = partial;
+        for (int jt = 0; jt < kMaxKeyTiles; ++jt) {
+            sum += s[jt][r];
         }
+        partial[r] = sum;
     }
-    // Quad swaps: lane c' ^ 1, then c' ^ 2 (r ^ 1, r ^ 2 within this lane).
-#pragma unroll
-    for (int a = 0; a < 4; ++a) {
-        float w[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) w[r] = v[a][r] + v[a][r ^ 1];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) v[a][r] = w[r] + w[r ^ 2];
-    }
-    // Half-row mirror: c' & 7 -> 7 - (c' & 7), i.e. group g ^ 1, element 3 - r.
-    {
-        float partner[4][4];
-#pragma unroll
-        for (int a = 0; a < 4; ++a)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) partner[a][r] = shuffle_xor(v[a][r], 16);
-#pragma unroll
-        for (int a = 0; a < 4; ++a)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) v[a][r] = v[a][r] + partner[a][3 - r];
-    }
-    // Row mirror: c' & 15 -> 15 - (c' & 15), i.e. group g ^ 3, element 3 - r.
-    {
-        float partner[4][4];
-#pragma unroll
-        for (int a = 0; a < 4; ++a)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) partner[a][r] = shuffle_xor(v[a][r], 48);
-#pragma unroll
-        for (int a = 0; a < 4; ++a)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) v[a][r] = v[a][r] + partner[a][3 - r];
-    }
-    // Every lane of a 16-lane row now holds that row's total; the four rows
-    // combine as (r0 + r1) + (r2 + r3).
-    const float inverse = 1.0F / ((v[0][0] + v[1][0]) + (v[2][0] + v[3][0]));
+    const float quad = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+    const float half = quad + shuffle_xor(quad, 16);
+    const float inverse = 1.0F / (half + shuffle_xor(half, 32));
 #pragma unroll
     for (int jt = 0; jt < kMaxKeyTiles; ++jt) {
 #pragma unroll

@@ -7,35 +7,33 @@
 //
 // Each row is reduced by a team of L lanes: column c is lane c % L's
 // (c / L)-th term, the lane folds its terms in order, then a fixed DPP tree
-// combines the team. The team width depends only on the element type and the
-// row width: bf16 rows up to 256 wide use 16-lane teams (four rows per
-// wavefront, one quarter of the reduction instructions per row), everything
-// else a full 64-lane wavefront. Measured on MI355X, the 16-lane teams cut the
-// [151296, 197] bf16 softmax from 41.9 us to 27 us, while fp32 at ViT-Tiny
-// batch 32 stays fastest on full wavefronts. Both paths below give a row the
-// same bits for a given (type, width), wherever the row sits in a launch,
-// which is what keeps a batch bitwise equal to its images run one at a time.
+// combines the team. The team width depends only on the row width: rows up to
+// 256 wide use 16-lane teams (four rows per wavefront, one quarter of the
+// reduction instructions per row), wider rows a full 64-lane wavefront.
+// Measured on MI355X, the 16-lane teams cut the [151296, 197] bf16 softmax
+// from 41.9 us to 27 us and the fp32 [18912, 197] one from 7.8 to 6.6 us. Both
+// paths below give a row the same bits for a given (type, width), wherever the
+// row sits in a launch, which is what keeps a batch bitwise equal to its
+// images run one at a time.
 //
 // Register path: each team loads its row's terms straight from HBM, keeps
 // them in registers from the max through the exponentials to the scaled
-// store, so HBM sees one read and one write per element. With full
-// wavefronts consecutive lanes read consecutive elements (one contiguous
-// 256-byte span per fp32 load instruction); rows of 197 floats are not
-// 16-byte aligned, and at ViT-Tiny batch 32 this beats staging through LDS
-// because it keeps more rows in flight per CU.
+// store, so HBM sees one read and one write per element. It takes wide rows
+// below the staged path's row count, and team-of-16 rows whose pointers are
+// not 16-byte aligned.
 //
-// Both of those paths read and write HBM with non-temporal loads and stores:
-// every line is read once and written once, and the pair skips allocating and
-// writing back lines the kernel will not touch again (ViT-Tiny batch 32
-// in place: 8.5 -> 7.8 us; the bf16 [151296, 197]: 28 -> 26 us). Plain
-// loads with non-temporal stores were slower than plain ones for both.
+// Both paths read and write HBM with non-temporal loads and stores: every
+// line is read once and written once, and the pair skips allocating and
+// writing back lines the kernel will not touch again (fp32 [18912, 197] in
+// place on full wavefronts: 8.5 -> 7.8 us; the bf16 [151296, 197]: 28 ->
+// 26 us). Plain loads with non-temporal stores were slower than plain ones.
 //
 // Staged path: R rows of any width are `columns` 16-byte vectors (R = 4 fp32,
 // 8 bf16), so each wavefront moves an R-row block between HBM and a
 // wave-private LDS tile with aligned dwordx4 traffic, and prefetches its next
 // block into registers while it reduces the current one out of LDS. It runs
-// for every bf16 team-of-16 row when the pointers allow and for wider or fp32
-// rows from a row count that fills the chip several times over.
+// for every team-of-16 row when the pointers allow and for wider rows from a
+// row count that fills the chip several times over.
 //
 // Exponentials are exp2((x - max) * log2(e)) on the hardware exp2. x - max is
 // exact at x = max, where the largest outputs sit, and the relative error of an
@@ -291,10 +289,8 @@ hipError_t launch_team(const T* input, T* output, int rows, int columns, hipStre
 
 template <typename T>
 hipError_t dispatch(const T* input, T* output, int rows, int columns, hipStream_t stream) {
-    if constexpr (sizeof(T) == 2) {
-        if (columns <= kTeamColumns) {
-            return launch_team<T, 16>(input, output, rows, columns, stream);
-        }
+    if (columns <= kTeamColumns) {
+        return launch_team<T, 16>(input, output, rows, columns, stream);
     }
     if (columns <= kWave * kMaxTerms) {
         return launch_team<T, kWave>(input, output, rows, columns, stream);
