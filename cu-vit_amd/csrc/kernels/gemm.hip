@@ -89,7 +89,10 @@ hipError_t launch(const T* a, const T* b, const float* bias, T* c, const GemmArg
     if (tiles > 0x7FFFFFFF) {
         return hipErrorInvalidConfiguration;
     }
-    auto kernel = gemm::gemm_kernel<T, WM, WN, TM, TN, BK, VecA, VecB, TransB, MinWaves>;
+    // The occupancy hint caps registers; the element-wise operand paths need
+    // more than it leaves, so they take the default.
+    constexpr int kMinWaves = VecA && VecB ? MinWaves : 1;
+    auto kernel = gemm::gemm_kernel<T, WM, WN, TM, TN, BK, VecA, VecB, TransB, kMinWaves>;
     // Above 64 KiB of LDS a kernel has to opt in, once per device.
     static std::atomic<std::uint64_t> opted_in{0};
     if (const hipError_t opted = allow_lds(reinterpret_cast<const void*>(kernel), S::kLdsBytes, opted_in);
