@@ -4,11 +4,14 @@
 // (DeviceBuffer, HostBuffer, Stream, DeviceArena, and VisionTransformer in
 // both precisions through the C++ API). The cases follow the reference's
 // tests/tensor_test.cu, device_buffer_test.cu, host_buffer_test.cu,
-// stream_test.cu, device_arena_test.cu, weights_test.cu and vit_test.cu.
+// stream_test.cu, device_arena_test.cu, weights_test.cu, vit_test.cu and
+// image_test.cu (PPM loading and argument checks on the host, preprocessing on
+// the device).
 #include "cuvit/device_arena.hpp"
 #include "cuvit/device_buffer.hpp"
 #include "cuvit/hip_check.hpp"
 #include "cuvit/host_buffer.hpp"
+#include "cuvit/image.hpp"
 #include "cuvit/kernels.hpp"
 #include "cuvit/stream.hpp"
 #include "cuvit/tensor.hpp"
@@ -21,6 +24,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <fstream>
 #include <functional>
 #include <iostream>
 #include <stdexcept>
@@ -537,6 +541,167 @@ int run(const std::vector<std::pair<std::string, std::function<void()>>>& cases)
     return failures == 0 ? 0 : 1;
 }
 
+// -- images (reference tests/image_test.cu) ----------------------------------
+
+void write_ppm(const std::string& path, int width, int height,
+               const std::vector<std::uint8_t>& pixels, const char* comment = nullptr) {
+    std::ofstream stream(path, std::ios::binary);
+    stream << "P6\n";
+    if (comment != nullptr) {
+        stream << '#' << comment << '\n';
+    }
+    stream << width << ' ' << height << "\n255\n";
+    stream.write(reinterpret_cast<const char*>(pixels.data()),
+                 static_cast<std::streamsize>(pixels.size()));
+}
+
+std::vector<std::uint8_t> ramp(int width, int height) {
+    std::vector<std::uint8_t> pixels(static_cast<std::size_t>(width) * height * 3);
+    for (int row = 0; row < height; ++row) {
+        for (int column = 0; column < width; ++column) {
+            const std::size_t at = (static_cast<std::size_t>(row) * width + column) * 3;
+            pixels[at] = static_cast<std::uint8_t>(column * 255 / (width - 1));
+            pixels[at + 1] = static_cast<std::uint8_t>(row * 255 / (height - 1));
+            pixels[at + 2] = 128;
+        }
+    }
+    return pixels;
+}
+
+void image_ppm_round_trip() {
+    const std::vector<std::uint8_t> pixels = ramp(7, 5);
+    write_ppm("plumbing_round_trip.ppm", 7, 5, pixels, " written by the test suite");
+    const cuvit::RgbImage image = cuvit::load_ppm("plumbing_round_trip.ppm");
+    require(image.width == 7 && image.height == 5, "the PPM header was misread");
+    require(image.pixels == pixels, "the PPM payload changed on the way through");
+    std::remove("plumbing_round_trip.ppm");
+}
+
+void image_malformed_files_are_rejected() {
+    require_throws<std::runtime_error>([] { static_cast<void>(cuvit::load_ppm("absent.ppm")); },
+                                       "a missing image was accepted");
+    {
+        std::ofstream ascii("plumbing_ascii.ppm");
+        ascii << "P3\n2 2\n255\n0 0 0 0 0 0 0 0 0 0 0 0\n";
+    }
+    require_throws<std::runtime_error>(
+        [] { static_cast<void>(cuvit::load_ppm("plumbing_ascii.ppm")); },
+        "an ASCII PPM was accepted as binary");
+    write_ppm("plumbing_short.ppm", 8, 8, std::vector<std::uint8_t>(8 * 8 * 3 - 32, 0));
+    require_throws<std::runtime_error>(
+        [] { static_cast<void>(cuvit::load_ppm("plumbing_short.ppm")); },
+        "a truncated image was accepted");
+    std::remove("plumbing_ascii.ppm");
+    std::remove("plumbing_short.ppm");
+}
+
+void image_invalid_settings_are_rejected() {
+    // Checked before any device work, so this runs without a GPU.
+    cuvit::RgbImage image;
+    image.width = 32;
+    image.height = 32;
+    image.pixels.assign(32 * 32 * 3, 100);
+    cuvit::Preprocessing settings;
+    settings.crop_fraction = 0.0F;
+    require_throws<std::invalid_argument>([&] { static_cast<void>(cuvit::preprocess(image, settings)); },
+                                          "a zero crop fraction was accepted");
+    settings = cuvit::Preprocessing{};
+    settings.stddev = {1.0F, 0.0F, 1.0F};
+    require_throws<std::invalid_argument>([&] { static_cast<void>(cuvit::preprocess(image, settings)); },
+                                          "a zero standard deviation was accepted");
+    settings = cuvit::Preprocessing{};
+    settings.size = 0;
+    require_throws<std::invalid_argument>([&] { static_cast<void>(cuvit::preprocess(image, settings)); },
+                                          "a zero size was accepted");
+    require_throws<std::invalid_argument>(
+        [] { static_cast<void>(cuvit::preprocess(cuvit::RgbImage{})); },
+        "an empty image was accepted");
+    require_throws<std::invalid_argument>(
+        [] { cuvit::launch_preprocess(nullptr, -1, 4, 4, nullptr); },
+        "a negative batch was accepted");
+    cuvit::launch_preprocess(nullptr, 0, 4, 4, nullptr); // an empty batch returns at once
+}
+
+void image_uniform_grey_normalises_to_one_value() {
+    cuvit::RgbImage image;
+    image.width = 300;
+    image.height = 300;
+    image.pixels.assign(300 * 300 * 3, 128);
+    const std::vector<float> tensor = cuvit::preprocess(image);
+    require(tensor.size() == 3U * 224 * 224, "the preprocessed tensor has the wrong size");
+    const float expected = (128.0F / 255.0F - 0.5F) / 0.5F;
+    for (const float value : tensor) {
+        require(std::fabs(value - expected) < 1.0e-5F,
+                "a uniform image did not normalize to a uniform value");
+    }
+}
+
+void image_channels_stay_planar() {
+    cuvit::RgbImage image;
+    image.width = 256;
+    image.height = 256;
+    image.pixels.resize(256 * 256 * 3);
+    for (std::size_t pixel = 0; pixel < 256U * 256; ++pixel) {
+        image.pixels[pixel * 3] = 255;
+        image.pixels[pixel * 3 + 1] = 0;
+        image.pixels[pixel * 3 + 2] = 128;
+    }
+    const std::vector<float> tensor = cuvit::preprocess(image);
+    const std::size_t plane = 224 * 224;
+    for (std::size_t i = 0; i < plane; ++i) {
+        require(std::fabs(tensor[i] - 1.0F) < 1.0e-5F, "the red plane is not saturated");
+        require(std::fabs(tensor[plane + i] + 1.0F) < 1.0e-5F, "the green plane is not empty");
+        require(std::fabs(tensor[2 * plane + i] - (128.0F / 255.0F - 0.5F) / 0.5F) < 1.0e-5F,
+                "the blue plane has the wrong value");
+    }
+}
+
+void image_centre_crop_keeps_the_middle() {
+    cuvit::RgbImage image;
+    image.width = 600;
+    image.height = 200;
+    image.pixels.assign(600 * 200 * 3, 0);
+    for (int row = 0; row < 200; ++row) {
+        for (int column = 250; column < 350; ++column) {
+            const std::size_t at = (static_cast<std::size_t>(row) * 600 + column) * 3;
+            image.pixels[at] = image.pixels[at + 1] = image.pixels[at + 2] = 255;
+        }
+    }
+    const std::vector<float> tensor = cuvit::preprocess(image);
+    require(tensor[112 * 224 + 112] > 0.9F, "the centre of the crop is not the centre of the image");
+    require(tensor[0] < -0.9F && tensor[224 * 224 - 1] < -0.9F, "the crop reached past the band");
+}
+
+void image_batch_equals_single_images() {
+    // launch_preprocess over two images in one launch, straight into a
+    // model-shaped input, gives each image's preprocess() bits.
+    cuvit::RgbImage first;
+    first.width = 320;
+    first.height = 240;
+    first.pixels = ramp(320, 240);
+    cuvit::RgbImage second = first;
+    for (std::size_t i = 0; i < second.pixels.size(); ++i) {
+        second.pixels[i] = static_cast<std::uint8_t>(second.pixels[i] * 7 + i);
+    }
+    const std::size_t bytes = first.pixels.size();
+    cuvit::DeviceBuffer<std::uint8_t> pixels(2 * bytes);
+    pixels.copy_from_host(first.pixels.data(), bytes);
+    pixels.copy_from_host(second.pixels.data(), bytes, bytes);
+    const std::size_t elements = 3 * 224 * 224;
+    cuvit::DeviceBuffer<float> tensor(2 * elements);
+    cuvit::Stream stream;
+    cuvit::launch_preprocess(pixels.data(), 2, 320, 240, tensor.data(), {}, stream.get());
+    stream.synchronize();
+    std::vector<float> both(2 * elements);
+    tensor.copy_to_host(both.data(), both.size());
+    const std::vector<float> a = cuvit::preprocess(first);
+    const std::vector<float> b = cuvit::preprocess(second);
+    require(std::memcmp(both.data(), a.data(), elements * sizeof(float)) == 0,
+            "image 0 of the batch differs from preprocess()");
+    require(std::memcmp(both.data() + elements, b.data(), elements * sizeof(float)) == 0,
+            "image 1 of the batch differs from preprocess()");
+}
+
 } // namespace
 
 int main(int argc, char** argv) {
@@ -551,14 +716,22 @@ int main(int argc, char** argv) {
                     {"hip_check_reports_the_error", hip_check_reports_the_error},
                     {"weights_round_trip_and_checks", weights_round_trip_and_checks},
                     {"vit_config_validation", vit_config_validation},
-                    {"arena_sizing", arena_sizing}});
+                    {"arena_sizing", arena_sizing},
+                    {"image_ppm_round_trip", image_ppm_round_trip},
+                    {"image_malformed_files_are_rejected", image_malformed_files_are_rejected},
+                    {"image_invalid_settings_are_rejected", image_invalid_settings_are_rejected}});
     }
     if (group == "device") {
         const int status = run({{"device_buffer_copies_and_bounds", device_buffer_copies_and_bounds},
                                 {"host_buffer_is_pinned_and_usable", host_buffer_is_pinned_and_usable},
                                 {"stream_pipeline", stream_pipeline},
                                 {"arena_carving", arena_carving},
-                                {"model_through_the_cpp_api", model_through_the_cpp_api}});
+                                {"model_through_the_cpp_api", model_through_the_cpp_api},
+                                {"image_uniform_grey_normalises_to_one_value",
+                                 image_uniform_grey_normalises_to_one_value},
+                                {"image_channels_stay_planar", image_channels_stay_planar},
+                                {"image_centre_crop_keeps_the_middle", image_centre_crop_keeps_the_middle},
+                                {"image_batch_equals_single_images", image_batch_equals_single_images}});
         // A kernel that faulted asynchronously would surface here.
         const hipError_t sync = hipDeviceSynchronize();
         if (sync != hipSuccess) {

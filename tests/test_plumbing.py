@@ -1,12 +1,13 @@
 """Runs the C++ plumbing tests (tests/cpp/plumbing_test.cpp).
 
 The `host` group needs no GPU: TensorView, launcher argument validation and
-exception mapping, HipError, weight files, VitConfig and arena sizing. The
-`device` group needs one: DeviceBuffer, HostBuffer (pinned), Stream,
-DeviceArena and VisionTransformer (fp32 and bf16, from float32 and bf16
-weight files) through the C++ API. They follow the reference's
-tests/tensor_test.cu, device_buffer_test.cu, host_buffer_test.cu,
-stream_test.cu, device_arena_test.cu, weights_test.cu and vit_test.cu.
+exception mapping, HipError, weight files, VitConfig, arena sizing, PPM
+loading and preprocessing's argument checks. The `device` group needs one:
+DeviceBuffer, HostBuffer (pinned), Stream, DeviceArena, VisionTransformer (fp32
+and bf16, from float32 and bf16 weight files) and preprocessing through the
+C++ API. They follow the reference's tests/tensor_test.cu,
+device_buffer_test.cu, host_buffer_test.cu, stream_test.cu,
+device_arena_test.cu, weights_test.cu, vit_test.cu and image_test.cu.
 """
 
 from __future__ import annotations
