@@ -240,6 +240,10 @@ int check_preprocess(const void* pixels, int batch, int width, int height,
     if (settings->size > kMaxPreprocessSize) {
         return fail(CUVIT_ERROR_LENGTH, "The preprocessing size exceeds the grid limit");
     }
+    if (saturating_product(saturating_product(saturating_product(batch, width), height), 3) ==
+        INT64_MAX) {
+        return fail(CUVIT_ERROR_LENGTH, "The preprocessing images exceed the addressable size");
+    }
     return ok();
 }
 

@@ -296,7 +296,8 @@ void cuvit_preprocessing_default(cuvit_preprocessing* settings);
  * Validation: batch 0 returns at once; then a negative batch, a null settings
  * pointer, the reference's four checks in its order (empty image, size,
  * crop fraction, zero stddev), null operands (all CUVIT_ERROR_INVALID_ARGUMENT),
- * and a size above 32768 (CUVIT_ERROR_LENGTH). The batch is an extension. */
+ * a size above 32768 and images whose bytes overflow int64 (CUVIT_ERROR_LENGTH).
+ * The batch is an extension. */
 int cuvit_preprocess_u8(const uint8_t* pixels, int batch, int width, int height,
                         const cuvit_preprocessing* settings, float* tensor,
                         cuvit_stream_t stream);

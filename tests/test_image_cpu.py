@@ -290,6 +290,8 @@ def test_preprocess_argument_checks(cuvit, lib):
         (dict(pixels=None), 1, "Preprocessing operands cannot be null"),
         (dict(tensor=None), 1, "Preprocessing operands cannot be null"),
         (dict(settings=P(size=32769)), 2, "The preprocessing size exceeds the grid limit"),
+        (dict(batch=2**30, width=2**31 - 1, height=2**31 - 1), 2,
+         "The preprocessing images exceed the addressable size"),
     ]
     for kwargs, status, message in cases:
         assert preprocess_status(cuvit, lib, **kwargs) == (status, message), kwargs
