@@ -1,5 +1,5 @@
 // CPU oracle for the layer-kernel path. TEST INFRASTRUCTURE ONLY (see
-// oracle.h): the checker for the HIP library, never part of it.
+// oracle.h): what the tests compare the HIP library against, never part of it.
 //
 // How each function is pinned (beyond restating the reference's loops):
 //   layer_norm, softmax, gelu, gemm, gemm_transposed, gemm_term_magnitudes

@@ -1,7 +1,7 @@
 /*
- * CPU oracle for the layer-kernel path. TEST INFRASTRUCTURE ONLY: it is the
- * checker that tests/, __graft_entry__.smoke() and bench.py's cpu_baseline use
- * against the HIP library. It is never linked into, or called by, the product.
+ * CPU oracle for the layer-kernel path. TEST INFRASTRUCTURE ONLY: tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline compare the HIP library
+ * against it. It is never linked into, or called by, the product.
  *
  * Every function restates the reference's CPU path in plain loops
  * (tests/reference/linear_algebra.hpp, tests/reference/vit.hpp,

@@ -1,13 +1,13 @@
 """numpy interface to the CPU oracle. TEST INFRASTRUCTURE ONLY.
 
 Imported by tests/, by __graft_entry__.smoke() and by bench.py's cpu_baseline
-leg, always as the checker (or the timed CPU baseline), never as the thing a
+leg, always as the comparison (or the timed CPU baseline), never as the thing a
 product path calls. Two libraries sit behind it:
 
 * liboracle.so - the restatement of the reference's CPU path (oracle.cpp);
 * _ref/libref.so - the reference's own tests/reference/*.hpp and
   src/runtime/weights.cpp compiled in place (only where /root/reference exists
-  at build time; the GPU box uses the prebuilt file if it travelled).
+  at build time; elsewhere the prebuilt file is used if present).
 """
 
 from __future__ import annotations

@@ -65,7 +65,7 @@ def compare_close(actual, expected, rtol: float = 1.0e-5, atol: float = 1.0e-6) 
     first_nonfinite = int(np.argmax(bad_nonfinite)) if bad_nonfinite.any() else a.size
     first_failing = int(np.argmax(failing)) if failing.any() else a.size
     stop = min(first_nonfinite, first_failing)
-    # The worst difference is tracked over the prefix the sequential checker
+    # The worst difference is tracked over the prefix the reference's sequential loop
     # would have scanned before stopping (test_utils.hpp:95-131).
     if stop > 0:
         window = rel[:stop] if stop < a.size else rel

@@ -3,7 +3,7 @@
 Mirrors the reference's tests/elementwise_test.cu case by case (shapes, seeds,
 distributions, tolerances), driving the HIP kernels through the C ABI and
 judging them against the oracle on the same seeded inputs. Added beyond the
-reference: the north_star bound max-abs <= 1e-5 for fp32 LN / softmax / GELU,
+reference: the bound max-abs <= 1e-5 for fp32 LN / softmax / GELU,
 in-place softmax, and the ViT-Tiny batch-32 shapes.
 """
 
@@ -18,7 +18,7 @@ from numerics import TestFailure, require_close, require_exact, require_max_abs
 
 pytestmark = pytest.mark.gpu
 
-MAX_ABS_FP32 = 1.0e-5  # north_star tolerance for LN, softmax and GELU in fp32
+MAX_ABS_FP32 = 1.0e-5  # stated tolerance for LN, softmax and GELU in fp32
 
 
 def require(condition, message):  # noqa: F811 - the reference's require()
