@@ -346,7 +346,8 @@ def counters(torch, cuvit, pools):
 def vit_base_bf16_counters(torch, cuvit, flush):
     """The ViT-Base batch-64 bf16 kernels for the counter passes, three cold
     launches each: LN [12608, 768], softmax [151296, 197] in place, the patch
-    gather [64, 3, 224, 224] and FC1 with the GELU epilogue."""
+    gather [64, 3, 224, 224], FC1 with the GELU epilogue and the fused
+    attention; then the fp32 fused attention at ViT-Tiny batch 32."""
     rows, embed, hidden, heads, batch = 64 * TOKENS, 768, 3072, 12, 64
     bf = torch.bfloat16
     x = torch.randn(rows * embed, device="cuda").to(bf)
@@ -361,12 +362,19 @@ def vit_base_bf16_counters(torch, cuvit, flush):
     c = torch.empty(rows * hidden, device="cuda", dtype=bf)
     problem = cuvit.gemm_problem(rows, hidden, embed, cuvit.TRANSPOSED)
     problem.epilogue.gelu = 1
+    qkv = torch.randn(rows * 3 * embed, device="cuda").to(bf)
+    context = torch.empty(rows * embed, device="cuda", dtype=bf)
+    tiny_qkv = torch.randn(BATCH * TOKENS * 3 * 192, device="cuda")
+    tiny_context = torch.empty(BATCH * TOKENS * 192, device="cuda")
     steps = {
         "bf16 layer_norm [12608,768]": lambda: cuvit.layer_norm(x, gamma, beta, y, rows, embed, 1e-6),
         "bf16 softmax [151296,197]": lambda: cuvit.softmax(logits, logits, batch * heads * TOKENS, TOKENS),
         "bf16 extract_patches b64": lambda: cuvit.extract_patches(images, patches, batch, CHANNELS,
                                                                   IMAGE, IMAGE, PATCH),
         "bf16 fc1_gelu_gemm 12608x3072x768": lambda: cuvit.gemm(x, w, bias, c, problem),
+        "bf16 attention ViT-Base b64": lambda: cuvit.attention(qkv, context, batch, heads, TOKENS, 64),
+        "fp32 attention ViT-Tiny b32": lambda: cuvit.attention(tiny_qkv, tiny_context, BATCH, 3,
+                                                               TOKENS, 64),
     }
     for name, launch in steps.items():
         for i in range(3):

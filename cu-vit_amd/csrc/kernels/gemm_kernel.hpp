@@ -216,7 +216,19 @@ template <typename T, int WM, int WN, int TM, int TN, int BK> struct Shape {
     static constexpr int kV = Mma<T>::kPerVec;
     static constexpr int kKBlock = gemm::kKBlock<T>;
     static_assert(BK % kKBlock == 0, "stages hold whole k-blocks");
-    static constexpr int kPitch = BK + kV;            // elements per LDS row (16 bytes of padding)
+    /// Rows of four 16-byte chunks (bf16 at BK = 32) are stored unpadded with
+    /// chunk c of row r at c ^ ((r >> 2) & 3). Measured with
+    /// SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE on gfx950 for the two access
+    /// patterns here, a stage write (lane l: row l / 4, chunk l % 4) and a
+    /// fragment read (lane l: row l % 32, chunk kb + l / 32):
+    ///   16-byte pad (80-byte rows)       reads 0,    writes 0.5
+    ///   unpadded, c ^ ((r >> 1) & 3)     reads 0.5,  writes 0
+    ///   unpadded, c ^ ((r >> 2) & 3)     reads 0,    writes 0
+    /// Rows of eight chunks keep the 16-byte pad (144-byte rows), which
+    /// measured 0 for both.
+    static constexpr bool kSwizzle = BK / kV == 4;
+    static_assert(!kSwizzle || kE % 16 == 0, "fragment rows keep their placement across MFMA tiles");
+    static constexpr int kPitch = kSwizzle ? BK : BK + kV; // elements per LDS row
     static constexpr int kChunksPerRow = BK / kV;     // 16-byte chunks per operand row of a stage
     static constexpr int kAChunks = kBM * kChunksPerRow;
     static constexpr int kBChunks = kBN * kChunksPerRow;
@@ -224,6 +236,15 @@ template <typename T, int WM, int WN, int TM, int TN, int BK> struct Shape {
     static constexpr int kBPerThread = (kBChunks + kThreads - 1) / kThreads;
     static constexpr int kStage = (kBM + kBN) * kPitch; // elements per LDS stage
     static constexpr std::size_t kLdsBytes = 2 * kStage * sizeof(T);
+
+    /// Where chunk @p chunk of operand row @p row sits in its LDS row.
+    __device__ __forceinline__ static int place(int row, int chunk) {
+        if constexpr (kSwizzle) {
+            return chunk ^ ((row >> 2) & 3);
+        } else {
+            return chunk;
+        }
+    }
 };
 
 /// Which tile a workgroup computes. With px * py == 8 the tile grid of an
@@ -379,7 +400,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(MinWav
             for (int p = 0; p < S::kAPerThread; ++p) {
                 const int q = t + kThreads * p;
                 if (S::kAChunks % kThreads == 0 || q < S::kAChunks) {
-                    store16(tile_a + (q / S::kChunksPerRow) * P + V * (q % S::kChunksPerRow), ra[p]);
+                    const int row = q / S::kChunksPerRow;
+                    store16(tile_a + row * P + V * S::place(row, q % S::kChunksPerRow), ra[p]);
                 }
             }
 #pragma unroll
@@ -387,15 +409,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(MinWav
                 const int q = t + kThreads * p;
                 if (S::kBChunks % kThreads == 0 || q < S::kBChunks) {
                     if constexpr (TransB) {
-                        store16(tile_b + (q / S::kChunksPerRow) * P + V * (q % S::kChunksPerRow),
-                                rb[p]);
+                        const int row = q / S::kChunksPerRow;
+                        store16(tile_b + row * P + V * S::place(row, q % S::kChunksPerRow), rb[p]);
                     } else {
                         // Scatter the chunk's V columns into k-contiguous rows.
                         const int kk = q / (BN / V);
                         const int n = V * (q % (BN / V));
 #pragma unroll
                         for (int e = 0; e < V; ++e) {
-                            Elem<T>::store_bits(tile_b + (n + e) * P + kk, rb[p], e);
+                            const int row = n + e;
+                            Elem<T>::store_bits(tile_b + row * P + V * S::place(row, kk / V) + kk % V,
+                                                rb[p], e);
                         }
                     }
                 }
@@ -409,7 +433,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(MinWav
                 lds + buffer * S::kStage + (BM + wave_n * TN * E + fragment_row) * P;
 #pragma unroll
             for (int kb = 0; kb < BK; kb += S::kKBlock) {
-                const int k = kb + V * fragment_chunk;
+                // Every fragment row is fragment_row modulo E, a multiple of
+                // the placement's 16-row period, so the lane's placement
+                // depends on fragment_row alone.
+                const int k = V * S::place(fragment_row, kb / V + fragment_chunk);
                 Vec16 fa[TM];
                 Vec16 fb[TN];
 #pragma unroll
