@@ -105,6 +105,22 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_kernel(const T* input, T*
 /// 64 * kPrefetch vectors, which covers every row the staged path takes.
 constexpr int kPrefetch = 4;
 
+/// Block row a team reduces in a pass. With four teams over the eight rows
+/// of a bf16 block, the passes take rows (0, 4, 1, 5), then (2, 6, 3, 7): at
+/// 197 columns the four teams' 16-element reads then fall on disjoint LDS
+/// banks (SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE of the [151296, 197]
+/// softmax 0.406 -> 0.000), where rows (0, 1, 2, 3) put teams 0 and 2, and
+/// 1 and 3, on common banks. Which team takes a row changes none of its bits.
+/// The four-row fp32 blocks have no such order: 197 * r mod 64 for four
+/// rows of a block never spreads four 16-bank runs apart.
+template <int kTeams, int R> __device__ __forceinline__ int team_row(int pass, int team) {
+    if constexpr (kTeams == 4 && R == 8) {
+        return 2 * pass + (team >> 1) + 4 * (team & 1);
+    } else {
+        return pass * kTeams + team;
+    }
+}
+
 template <typename T, int L, int J>
 __global__ __launch_bounds__(kBlock) void softmax_staged_kernel(const T* input, T* output, int rows,
                                                                 int columns) {
@@ -168,7 +184,7 @@ __global__ __launch_bounds__(kBlock) void softmax_staged_kernel(const T* input, 
         // reductions need no barrier between them.
 #pragma unroll
         for (int pass = 0; pass < kPasses; ++pass) {
-            const int r = pass * kTeams + lane / L;
+            const int r = team_row<kTeams, R>(pass, lane / L);
             const bool here = r < rows_here;
             float x[J];
 #pragma unroll

@@ -41,7 +41,7 @@ def test_layer_norm_bf16(cuvit, oracle, device, rows, columns):
 
 
 @pytest.mark.parametrize("rows,columns", [(151296, 197), (591, 197), (7, 197), (3, 1000),
-                                          (2, 1500), (4, 1)])
+                                          (2, 1500), (4, 1), (16, 3), (24, 128), (40, 65)])
 @pytest.mark.parametrize("in_place", [False, True])
 def test_softmax_bf16(cuvit, oracle, device, rows, columns, in_place):
     bits, values = bf16_inputs(oracle, 505 + rows, rows * columns)

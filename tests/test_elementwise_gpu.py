@@ -173,7 +173,10 @@ SOFTMAX_SHAPES = [(1, 2), (197, 197), (4, 1), (3, 1000), (8, 33),
                   # beyond the reference: one attention head-batch, tails of 4-row blocks,
                   # widths across the register-resident limit
                   (591, 197), (5, 197), (6, 197), (7, 197), (13, 64), (3, 1024), (2, 1025),
-                  (9, 2500), (4, 255)]
+                  (9, 2500), (4, 255),
+                  # LDS tile rows padded to keep the row teams on disjoint banks, vectors
+                  # straddling two or more rows
+                  (6, 128), (11, 7), (9, 3)]
 
 
 @pytest.mark.parametrize("rows,columns", SOFTMAX_SHAPES)
