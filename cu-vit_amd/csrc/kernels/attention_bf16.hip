@@ -34,11 +34,20 @@
 //
 // Layout: qkv is [images, tokens, 3, heads, 64] and context is
 // [images, tokens, heads, 64], bf16. A workgroup owns one (image, head) and
-// `waves` query tiles of 32 rows, one per wavefront. V of the (image, head)
-// sits in LDS transposed, [64][keys + 8], so a lane's weights.V B fragment is
-// 16 contiguous bytes, and K as [keys][64 + 8]; with the padding, 16
-// consecutive rows hit distinct bank quads. Q fragments are read straight
-// from global memory (16 contiguous bytes).
+// `waves` query tiles of 32 rows, one per wavefront. K of the (image, head)
+// sits in LDS as [keys][64 + 8]; with the padding, 16 consecutive rows hit
+// distinct bank quads. V sits as [keys][64], unpadded, its 16-byte chunk m of
+// key k at chunk m ^ 4 ((k >> 1) & 1), and a lane's weights.V B fragment (8
+// consecutive keys of one dim) comes from two ds_read_b64_tr_b16, the LDS
+// read that transposes 16-bit elements within each 16 lanes: lane i of a
+// group receives element i % 4 of the 8 bytes lane 4 e + i / 4 addressed, as
+// its element e. With lane j of a group addressing key base + j / 4, dims
+// 4 (j % 4) + 0..3, lane i gets dim i of keys base + 0..3. The 32 lanes of
+// a half-wavefront read four keys' 32 dims, which the placement spreads over
+// all 64 banks, and the stores from global memory write whole 16-byte chunks
+// (the transposed layout this replaces took eight 2-byte stores a chunk,
+// about half of the kernel's LDS cycles lost to bank conflicts). Q fragments
+// are read straight from global memory (16 contiguous bytes).
 #include "device_common.hpp"
 #include "gemm_kernel.hpp"
 #include "launch.hpp"
@@ -64,16 +73,45 @@ constexpr int kMaxKeyTiles = kMaxTokens / kEdge;
 constexpr int kMaxWaves = 8;
 constexpr int kWavesPerGroup = 4;
 
-/// Elements per LDS row of transposed V for @p key_tiles 32-key tiles.
-__host__ __device__ constexpr int row_pitch(int key_tiles) { return key_tiles * kEdge + 8; }
 /// Elements per LDS row of K ([key][head_dim + 8]).
 constexpr int kKeyPitch = kHeadDim + 8;
 
-/// Transposed V, then K.
+/// V ([key][head_dim]), then K.
 __host__ __device__ constexpr std::size_t lds_bytes(int key_tiles) {
-    return (static_cast<std::size_t>(kHeadDim) * row_pitch(key_tiles) +
-            static_cast<std::size_t>(key_tiles) * kEdge * kKeyPitch) *
-           2;
+    return static_cast<std::size_t>(key_tiles) * kEdge * (kHeadDim + kKeyPitch) * 2;
+}
+
+/// Element offset of V[key][dim] in its LDS tile: 16-byte chunk dim / 8 of
+/// the key's row sits at chunk (dim / 8) ^ 4 ((key >> 1) & 1).
+__device__ __forceinline__ int value_slot(int key, int dim) {
+    return key * kHeadDim + 8 * ((dim >> 3) ^ (4 * ((key >> 1) & 1))) + (dim & 7);
+}
+
+/// Four 16-bit elements in LDS, the operand type of ds_read_b64_tr_b16.
+typedef short Short4 __attribute__((vector_size(4 * sizeof(short))));
+using Lds4x16 = __attribute__((address_space(3))) Short4;
+
+/// The weights.V B fragment of k-block @p kb, dims @p d0 + 0..31: lane l
+/// holds dim d0 + l % 32, keys 16 kb + 8 (l / 32) + 0..7, the layout a
+/// 16-byte row of transposed V would give it.
+__device__ __forceinline__ Vec16 value_fragment(const std::uint16_t* values, int kb, int d0,
+                                                int lane) {
+    const int j = lane & 15;
+    const int dim = d0 + 16 * ((lane >> 4) & 1) + 4 * (j & 3);
+    Vec16 fragment;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const int key = kb * 16 + 8 * (lane >> 5) + 4 * s + (j >> 2);
+        // `values` points into LDS; the C-style cast is the address-space
+        // conversion the builtin's operand needs.
+        const auto part =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((Lds4x16*)(values + value_slot(key, dim)));
+        fragment.w[2 * s] = static_cast<std::uint16_t>(part[0]) |
+                            (static_cast<std::uint32_t>(static_cast<std::uint16_t>(part[1])) << 16);
+        fragment.w[2 * s + 1] = static_cast<std::uint16_t>(part[2]) |
+                                (static_cast<std::uint32_t>(static_cast<std::uint16_t>(part[3])) << 16);
+    }
+    return fragment;
 }
 
 /// 16 bytes at @p element of @p base, or zero when @p inside is false.
@@ -98,10 +136,9 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
     const std::uint16_t* __restrict__ qkv, std::uint16_t* __restrict__ context, int heads,
     int tokens, float scale) {
     constexpr int kPadded = KT * kEdge;
-    constexpr int kPitch = row_pitch(KT);
     extern __shared__ Vec16 lds_vectors[];
-    std::uint16_t* const values = reinterpret_cast<std::uint16_t*>(lds_vectors); // [64][kPitch]
-    std::uint16_t* const keys = values + kHeadDim * kPitch;                      // [kPadded][72]
+    std::uint16_t* const values = reinterpret_cast<std::uint16_t*>(lds_vectors); // [kPadded][64]
+    std::uint16_t* const keys = values + kPadded * kHeadDim;                     // [kPadded][72]
     const int waves = static_cast<int>(blockDim.x) / kWave;
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     const int lane = lane_id();
@@ -119,18 +156,15 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
     const std::uint16_t* const k_base = q_base + embed;
     const std::uint16_t* const v_base = q_base + 2 * embed;
 
-    // V transposed and K as is into LDS, shared by the workgroup's query
-    // tiles; keys past the tokens are zero.
+    // V and K into LDS, shared by the workgroup's query tiles; keys past the
+    // tokens are zero.
     constexpr int kChunks = kHeadDim / 8;
     for (int c = threadIdx.x; c < kPadded * kChunks; c += blockDim.x) {
         const int key = c / kChunks;
         const int d0 = 8 * (c % kChunks);
         const Vec16 v = load_or_zero(v_base, key * qkv_row + d0, key < tokens);
         const Vec16 k = load_or_zero(k_base, key * qkv_row + d0, key < tokens);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            Elem<std::uint16_t>::store_bits(values + (d0 + e) * kPitch + key, v, e);
-        }
+        store16(values + value_slot(key, d0), v);
         store16(keys + key * kKeyPitch + d0, k);
     }
     __syncthreads();
@@ -255,7 +289,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
 #pragma unroll
         for (int kb = 0; kb < kBlocks; ++kb) {
             if (kb < 2 * KT) {
-                const Vec16 v = load16(values + (d0 + row) * kPitch + kb * kKBlock + chunk);
+                const Vec16 v = value_fragment(values, kb, d0, lane);
                 Bf16Mma::run(acc, v, fragment[kb]);
             } else {
                 const Vec16 zero{{0U, 0U, 0U, 0U}};
