@@ -183,6 +183,15 @@ def copy_ceiling(torch, device, nbytes: int) -> float:
     return ms
 
 
+def launch_floor(torch, device) -> float:
+    """ms per launch of a kernel with (almost) nothing to do: a one-element
+    fill, back-to-back in one graph. Every dependent launch pays it, whatever
+    its size: the dispatch, the end-of-kernel release and the next launch's
+    wait."""
+    x = torch.empty(1, device=device)
+    return timed_graph(torch, lambda: [x.fill_(0.0) for _ in range(200)], 4) / 200
+
+
 def vit_config(cuvit, base: bool):
     """ViT-Tiny/16 (VitConfig's defaults) or ViT-Base/16 (E 768, 12 heads, MLP 3072)."""
     config = cuvit.default_config()
@@ -532,6 +541,16 @@ def main():
                      "traffic": measured_traffic().get(dominant),
                      "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT)},
         "kernels": kernels,
+    }
+    floor_ms = launch_floor(torch, device)
+    step_launches = 5
+    line["launch_floor"] = {
+        "us_per_launch": round(floor_ms * 1e3, 3),
+        "what": "a one-element torch fill, back-to-back in one HIP graph",
+        "step_launches": step_launches,
+        "step_us_above_floor": round((ms_per_step - step_launches * floor_ms) * 1e3, 3),
+        "step_GBps_above_floor": round(
+            STEP_BYTES / ((ms_per_step - step_launches * floor_ms) * 1e-3) / 1e9, 1),
     }
     model_ms, flops = vit_forward(torch, cuvit, device, BATCH, 20)
     line["vit_tiny_forward"] = {
