@@ -232,3 +232,43 @@ def test_model_precision_is_validated_before_any_allocation(cuvit, lib, tmp_path
     assert not handle.value
     assert lib.cuvit_vit_precision(None) == -1
     assert (cuvit.PRECISION_F32, cuvit.PRECISION_BF16) == (0, 1)
+
+
+def test_last_error_belongs_to_the_calling_thread(cuvit):
+    """Launchers may be called from any host thread (kernels.hpp: stateless,
+    re-entrant), so the message a failing call leaves behind is its own
+    thread's. Four threads each fail in their own way 500 times, concurrently;
+    ctypes releases the interpreter lock around both the failing call and the
+    message read, so a shared message would show up here as another thread's."""
+    import threading
+
+    cases = [
+        (lambda: cuvit.layer_norm(FAKE, FAKE, FAKE, FAKE, -1, 4),
+         "Layer norm dimensions cannot be negative"),
+        (lambda: cuvit.softmax(None, None, 2, 3), "Softmax operands cannot be null"),
+        (lambda: cuvit.gelu(FAKE, FAKE, -5), "GELU element count cannot be negative"),
+        (lambda: cuvit.extract_patches(FAKE, FAKE, 1, 3, 10, 10, 4),
+         "Patch extraction needs the image to divide into whole patches"),
+    ]
+    barrier = threading.Barrier(len(cases))
+    failures = []
+
+    def run(call, expected):
+        barrier.wait()
+        for _ in range(500):
+            try:
+                call()
+            except cuvit.InvalidArgument as error:
+                if expected not in str(error):
+                    failures.append(f"expected {expected!r}, got {error}")
+                    return
+            else:
+                failures.append(f"no error for {expected!r}")
+                return
+
+    threads = [threading.Thread(target=run, args=case) for case in cases]
+    for thread in threads:
+        thread.start()
+    for thread in threads:
+        thread.join()
+    assert not failures, failures[:3]
