@@ -5,7 +5,7 @@ blocks (src/kernels/normalization.cu:214-220), so each of these sizes is a
 valid call there too. Each test sits just past 2^31 elements and checks the
 rows that straddle element 2^31, the first and last rows and a random sample,
 against the closed form (gather, broadcast, add: bit-exact) or the oracle
-(LayerNorm, softmax). About 26 GB of device memory per test, freed after it.
+(LayerNorm, softmax). At most about 20 GB of device memory per test, freed after it.
 """
 
 from __future__ import annotations
