@@ -1,11 +1,11 @@
 """Operands beyond 2^31 elements: the gather, LayerNorm, softmax, class-token
-broadcast and positional add address them with 64-bit offsets. The
+broadcast, positional add and the GEMM address them with 64-bit offsets. The
 reference's launchers take 64-bit counts and reject only grids above 2^31 - 1
 blocks (src/kernels/normalization.cu:214-220), so each of these sizes is a
 valid call there too. Each test sits just past 2^31 elements and checks the
 rows that straddle element 2^31, the first and last rows and a random sample,
 against the closed form (gather, broadcast, add: bit-exact) or the oracle
-(LayerNorm, softmax). At most about 20 GB of device memory per test, freed after it.
+(LayerNorm, softmax, GEMM). At most about 20 GB of device memory per test, freed after it.
 """
 
 from __future__ import annotations
@@ -127,3 +127,27 @@ def test_class_token_and_positional_add_beyond_2_31_elements(cuvit, device):
     expected = expected + to_host(pos).reshape(TOKENS, EMBED)
     actual = take_rows(tokens, per_image, picked).reshape(-1, TOKENS, EMBED)
     assert np.array_equal(actual.view(np.uint32), expected.astype(np.float32).view(np.uint32))
+
+
+def test_gemm_gelu_with_a_beyond_2_31_elements(cuvit, oracle, device):
+    """FC1's epilogue (bias, erf-GELU) on A [m, 768] with m * 768 > 2^31: the
+    rows past element 2^31 of A, and their outputs, against the oracle's
+    gemm_transposed + gelu at the GELU tolerance of the GEMM tests."""
+    from numerics import require_close
+
+    m, n, k = LIMIT // 768 + 32, 64, 768
+    assert m * k > LIMIT
+    print(f"gemm + GELU: {m} x {n} x {k}", flush=True)
+    torch.manual_seed(8)
+    a = torch.randn(m * k, device=device)
+    w = torch.randn(n * k, device=device) * 0.02
+    bias = torch.randn(n, device=device) * 0.02
+    c = torch.full((m * n,), float("nan"), device=device)
+    problem = cuvit.gemm_problem(m, n, k, cuvit.TRANSPOSED)
+    problem.epilogue.gelu = 1
+    cuvit.gemm(a, w, bias, c, problem)
+    torch.cuda.synchronize()
+    picked = rows_around(LIMIT // k, m, np.random.default_rng(35))
+    pre = oracle.gemm_transposed(take_rows(a, k, picked), to_host(w), to_host(bias), picked.size, n, k)
+    require_close(take_rows(c, n, picked), oracle.gelu(pre), "GEMM past 2^31 elements of A",
+                  1.0e-4, 1.0e-5)
