@@ -151,3 +151,55 @@ def test_gemm_gelu_with_a_beyond_2_31_elements(cuvit, oracle, device):
     pre = oracle.gemm_transposed(take_rows(a, k, picked), to_host(w), to_host(bias), picked.size, n, k)
     require_close(take_rows(c, n, picked), oracle.gelu(pre), "GEMM past 2^31 elements of A",
                   1.0e-4, 1.0e-5)
+
+
+def test_bf16_gather_beyond_2_31_elements(cuvit, device):
+    """The bf16 gather (two 16-byte vectors per patch row) at the element
+    count of the fp32 test: each element holds the low 16 bits of its flat
+    index, so every output element must hold its source's."""
+    per_image = 3 * IMAGE * IMAGE
+    batch = LIMIT // per_image + 6
+    total = batch * per_image
+    print(f"bf16 gather: {batch} images, {total} elements", flush=True)
+    images = torch.empty(total, dtype=torch.int16, device=device)
+    chunk = 1 << 28
+    for start in range(0, total, chunk):
+        end = min(total, start + chunk)
+        images[start:end] = torch.arange(start, end, dtype=torch.int64, device=device).to(torch.int16)
+    patches = torch.full((total,), -1, dtype=torch.int16, device=device)
+    cuvit.extract_patches(images.view(torch.bfloat16), patches.view(torch.bfloat16), batch, 3,
+                          IMAGE, IMAGE, PATCH)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(36)
+    positions = np.concatenate([
+        np.arange(LIMIT - 4096, LIMIT + 4096), np.arange(total - 4096, total),
+        rng.integers(0, total, 1 << 20)]).astype(np.int64)
+    row, element = positions // 768, positions % 768
+    image, patch = row // 196, row % 196
+    channel, within = element // 256, element % 256
+    source = (((image * 3 + channel) * IMAGE + (patch // 14) * PATCH + within // PATCH) * IMAGE +
+              (patch % 14) * PATCH + within % PATCH)
+    expected = source.astype(np.uint64).astype(np.uint16).view(np.int16)
+    actual = to_host(patches[torch.from_numpy(positions).to(device)])
+    assert np.array_equal(actual, expected)
+
+
+def test_bf16_softmax_beyond_2_31_elements_in_place(cuvit, oracle, device):
+    """The bf16 staged softmax (eight-row blocks) past 2^31 elements, against
+    the oracle on the bf16 inputs at the bf16 tolerance."""
+    from numerics import require_close
+    from oracle import bf16_to_float
+
+    rows = LIMIT // TOKENS + 66
+    print(f"bf16 softmax: [{rows}, {TOKENS}] in place", flush=True)
+    torch.manual_seed(9)
+    logits = torch.randn(rows * TOKENS, device=device).to(torch.bfloat16)
+    picked = rows_around(LIMIT // TOKENS, rows, np.random.default_rng(37))
+    index = torch.from_numpy(picked).to(device)
+    before = to_host(logits.view(-1, TOKENS).index_select(0, index).view(torch.int16))
+    expected = oracle.softmax(bf16_to_float(before.view(np.uint16)))
+    cuvit.softmax(logits, logits, rows, TOKENS)
+    torch.cuda.synchronize()
+    after = to_host(logits.view(-1, TOKENS).index_select(0, index).view(torch.int16))
+    require_close(bf16_to_float(after.view(np.uint16)), expected, "bf16 softmax past 2^31", 1.0e-2,
+                  1.0e-6)
