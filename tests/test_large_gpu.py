@@ -203,3 +203,26 @@ def test_bf16_softmax_beyond_2_31_elements_in_place(cuvit, oracle, device):
     after = to_host(logits.view(-1, TOKENS).index_select(0, index).view(torch.int16))
     require_close(bf16_to_float(after.view(np.uint16)), expected, "bf16 softmax past 2^31", 1.0e-2,
                   1.0e-6)
+
+
+def test_bf16_layer_norm_beyond_2_31_elements(cuvit, oracle, device):
+    """The bf16 LayerNorm (fp32 statistics, one rounding at the store) past 2^31
+    elements, against the oracle on the bf16 inputs at the bf16 tolerance."""
+    from numerics import require_close
+    from oracle import bf16_to_float
+
+    rows = LIMIT // EMBED + 86
+    print(f"bf16 layer norm: [{rows}, {EMBED}]", flush=True)
+    torch.manual_seed(10)
+    x = torch.randn(rows * EMBED, device=device).to(torch.bfloat16)
+    gamma = torch.randn(EMBED, device=device) * 0.02 + 1.0
+    beta = torch.randn(EMBED, device=device) * 0.02
+    y = torch.empty_like(x)
+    cuvit.layer_norm(x, gamma, beta, y, rows, EMBED, 1e-6)
+    torch.cuda.synchronize()
+    picked = rows_around(LIMIT // EMBED, rows, np.random.default_rng(38))
+    index = torch.from_numpy(picked).to(device)
+    inputs = to_host(x.view(-1, EMBED).index_select(0, index).view(torch.int16)).view(np.uint16)
+    outputs = to_host(y.view(-1, EMBED).index_select(0, index).view(torch.int16)).view(np.uint16)
+    expected = oracle.layer_norm(bf16_to_float(inputs), to_host(gamma), to_host(beta), 1e-6)
+    require_close(bf16_to_float(outputs), expected, "bf16 layer norm past 2^31", 1.0e-2, 1.0e-3)
