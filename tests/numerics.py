@@ -51,6 +51,19 @@ def _flat(x) -> np.ndarray:
     return np.asarray(x, dtype=np.float64).reshape(-1)
 
 
+def _track_worst(result: Comparison, rel: np.ndarray, stop: int, first_failing: int) -> None:
+    """The worst relative difference over the elements the reference's sequential
+    loop records before it returns (test_utils.hpp:95-131): every element before
+    the stop, plus the stopping element itself when it fails on tolerance (the
+    loop records it before the check), not when it is non-finite (returned
+    before). Ties keep the first index, as the loop's strict `>` does."""
+    scanned = stop + 1 if stop < rel.size and stop == first_failing else stop
+    if scanned > 0:
+        window = rel[:scanned]
+        result.worst_index = int(np.argmax(window))
+        result.worst_relative_difference = float(window[result.worst_index])
+
+
 def compare_close(actual, expected, rtol: float = 1.0e-5, atol: float = 1.0e-6) -> Comparison:
     a, e = _flat(actual), _flat(expected)
     assert a.size == e.size, "compared sequences differ in length"
@@ -58,19 +71,15 @@ def compare_close(actual, expected, rtol: float = 1.0e-5, atol: float = 1.0e-6) 
     finite = np.isfinite(a) & np.isfinite(e)
     same_infinity = np.isinf(a) & np.isinf(e) & (np.signbit(a) == np.signbit(e))
     bad_nonfinite = ~finite & ~same_infinity
-    diff = np.where(finite, np.abs(a - e), 0.0)
+    with np.errstate(invalid="ignore"):
+        diff = np.where(finite, np.abs(a - e), 0.0)
     mag = np.where(finite, np.abs(e), 0.0)
     rel = np.where(mag > 0, diff / np.where(mag > 0, mag, 1.0), diff)
     failing = finite & (diff > atol + rtol * mag)
     first_nonfinite = int(np.argmax(bad_nonfinite)) if bad_nonfinite.any() else a.size
     first_failing = int(np.argmax(failing)) if failing.any() else a.size
     stop = min(first_nonfinite, first_failing)
-    # The worst difference is tracked over the prefix the reference's sequential loop
-    # would have scanned before stopping (test_utils.hpp:95-131).
-    if stop > 0:
-        window = rel[:stop] if stop < a.size else rel
-        result.worst_index = int(np.argmax(window))
-        result.worst_relative_difference = float(window[result.worst_index])
+    _track_worst(result, rel, stop, first_failing)
     if stop == a.size:
         return result
     result.matched = False
@@ -92,17 +101,15 @@ def compare_close_scaled(actual, expected, scale, rtol: float = 1.0e-6,
     result = Comparison()
     bad_nonfinite = ~(np.isfinite(a) & np.isfinite(e) & np.isfinite(s))
     finite = ~bad_nonfinite
-    diff = np.where(finite, np.abs(a - e), 0.0)
+    with np.errstate(invalid="ignore"):
+        diff = np.where(finite, np.abs(a - e), 0.0)
     mag = np.where(finite, s, 0.0)
     rel = np.where(mag > 0, diff / np.where(mag > 0, mag, 1.0), diff)
     failing = finite & (diff > atol + rtol * mag)
     first_nonfinite = int(np.argmax(bad_nonfinite)) if bad_nonfinite.any() else a.size
     first_failing = int(np.argmax(failing)) if failing.any() else a.size
     stop = min(first_nonfinite, first_failing)
-    if stop > 0:
-        window = rel[:stop] if stop < a.size else rel
-        result.worst_index = int(np.argmax(window))
-        result.worst_relative_difference = float(window[result.worst_index])
+    _track_worst(result, rel, stop, first_failing)
     if stop == a.size:
         return result
     result.matched = False
