@@ -7,9 +7,18 @@ One step is one pass of the path over one batch:
   class token    cls[192] -> row 0 of each image's tokens[32, 197, 192]
   positional add tokens[32, 197, 192] += pos[197, 192]
 
-Inputs are synthetic (seeded device RNG), resident in HBM before timing.
-Every kernel cycles through its own pool of buffer sets larger than twice the
-256 MB Infinity Cache, so each launch reads and writes cold HBM.
+Inputs are synthetic, drawn on the host from the reference tests' DataGenerator
+streams (LayerNorm seed 101 at batch 32, softmax seed 202, gather / class token
+/ positional add seed 303; oracle/workloads.py holds the draw order) and copied
+into HBM before timing. Every kernel cycles through its own pool of buffer sets,
+each a copy of those inputs, larger than twice the 256 MB Infinity Cache, so
+each launch reads and writes cold HBM.
+
+Checked: before timing, one step's outputs are compared with the CPU oracle on
+the same inputs (gather, class token and positional add bit-exact; LayerNorm
+and softmax max-abs <= 1e-5); after timing, every set's gather and LayerNorm
+outputs again, each image's class-token row bit-exact, and every softmax row
+summing to one. A mismatch exits with status 3 and prints no JSON line.
 
 value        algorithmic bytes of one step / measured time of one step (GB/s);
              the K timed steps are one captured HIP graph, timed with HIP events
@@ -17,15 +26,17 @@ value        algorithmic bytes of one step / measured time of one step (GB/s);
 roofline     the kernel with the largest share of the step: algorithmic bytes of
              one launch / its average launch duration, from HIP events around
              a graph of back-to-back launches of that kernel over its pool.
-copy ceiling a device-to-device copy of the same bytes over the same kind of
-             cold pools, per kernel: what any kernel of that size can reach.
+copy ceiling the library's bench-only copy kernel (libcuvit_bench.so: eight
+             256-thread workgroups per CU, four 16-byte non-temporal vectors
+             per thread) moving the same bytes over the same kind of cold
+             pools, per kernel: what a kernel of that size can reach here.
 vit_tiny_forward  the full batch-32 forward (89 launches: attention fused, positional add in the embedding GEMM) as one HIP graph.
 vit_*_forward_bf16 the bf16 model: ViT-Tiny at batch 32 and ViT-Base at batch 64.
 vit_base_b64_bf16 the bf16 twins at ViT-Base/16 batch-64 shapes, cold.
 size_sweep   LN, softmax and the gather at ViT-Tiny shapes for batches 32-1024,
              each beside a same-bytes copy.
-cpu_baseline the CPU oracle (a restatement of the reference's CPU loops) on a
-             bounded sample of the same workload, one core.
+cpu_baseline the CPU oracle (a restatement of the reference's CPU loops) on
+             the same seeded inputs, whole steps until a time bound, one core.
 
 Modes: --mode bench (default) prints the JSON line; --mode counters runs a plain
 device copy of known size and then each kernel over cold buffers, for
@@ -96,34 +107,34 @@ def parse():
 
 
 class Pools:
-    """Rotating buffer sets, one pool per kernel, each > POOL_BYTES."""
+    """Rotating buffer sets, one pool per kernel, each > POOL_BYTES; every set
+    of a pool holds the same seeded inputs."""
 
-    def __init__(self, torch, device):
+    def __init__(self, torch, device, inputs):
         def sets(per_set_bytes):
             return max(2, -(-POOL_BYTES // per_set_bytes))
 
-        gen = torch.Generator(device=device)
-        gen.manual_seed(101)
+        def copies(array, count):
+            first = torch.from_numpy(array.reshape(-1)).to(device)
+            return [first] + [first.clone() for _ in range(count - 1)]
+
         self.ln_sets = sets(BYTES["layer_norm"])
-        self.ln_x = [torch.randn(ROWS * EMBED, device=device, generator=gen) for _ in range(self.ln_sets)]
-        self.ln_y = [torch.empty(ROWS * EMBED, device=device) for _ in range(self.ln_sets)]
-        self.gamma = 1.0 + 0.02 * torch.randn(EMBED, device=device, generator=gen)
-        self.beta = 0.02 * torch.randn(EMBED, device=device, generator=gen)
-        gen.manual_seed(202)
+        self.ln_x = copies(inputs["ln_x"], self.ln_sets)
+        self.ln_y = [torch.full((ROWS * EMBED,), float("nan"), device=device)
+                     for _ in range(self.ln_sets)]
+        self.gamma = torch.from_numpy(inputs["gamma"]).to(device)
+        self.beta = torch.from_numpy(inputs["beta"]).to(device)
         self.sm_sets = sets(BYTES["softmax"])
-        self.logits = [torch.randn(SOFTMAX_ROWS * TOKENS, device=device, generator=gen)
-                       for _ in range(self.sm_sets)]
-        gen.manual_seed(303)
+        self.logits = copies(inputs["logits"], self.sm_sets)
         self.px_sets = sets(BYTES["extract_patches"])
-        self.images = [torch.rand(BATCH * CHANNELS * IMAGE * IMAGE, device=device, generator=gen) * 2 - 1
-                       for _ in range(self.px_sets)]
-        self.patches = [torch.empty(BATCH * PATCHES * PATCH_ELEMENTS, device=device)
+        self.images = copies(inputs["images"], self.px_sets)
+        self.patches = [torch.full((BATCH * PATCHES * PATCH_ELEMENTS,), float("nan"), device=device)
                         for _ in range(self.px_sets)]
         self.tok_sets = sets(BYTES["add_broadcast"])
-        self.tokens = [torch.randn(BATCH * TOKENS * EMBED, device=device, generator=gen)
+        self.tokens = [torch.zeros(BATCH * TOKENS * EMBED, device=device)
                        for _ in range(self.tok_sets)]
-        self.pos = 0.02 * torch.randn(TOKENS * EMBED, device=device, generator=gen)
-        self.cls = 0.02 * torch.randn(EMBED, device=device, generator=gen)
+        self.pos = torch.from_numpy(inputs["pos"]).to(device)
+        self.cls = torch.from_numpy(inputs["cls"]).to(device)
 
     def launchers(self, cuvit):
         """name -> function(set_index) that enqueues one launch on the current stream."""
@@ -141,6 +152,107 @@ class Pools:
             "add_broadcast": lambda i: cuvit.add_broadcast(
                 self.tokens[i % self.tok_sets], self.pos, TOKENS * EMBED, BATCH),
         }
+
+
+def seeded_inputs():
+    """The checking leg's oracle and the step's inputs, drawn from the
+    DataGenerator streams of oracle/workloads.py."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import workloads
+    from oracle import Oracle
+
+    oracle = Oracle()
+    c1 = workloads.layer_norm_c1(oracle, ROWS)
+    c3 = workloads.tokens_c3(oracle, BATCH)
+    inputs = {"ln_x": c1["x"], "gamma": c1["gamma"], "beta": c1["beta"],
+              "logits": workloads.softmax_c2(oracle), "images": c3["images"],
+              "pos": c3["pos"], "cls": c3["cls"]}
+    return oracle, inputs
+
+
+def expected_step(oracle, inputs):
+    """The oracle's outputs of one step on fresh inputs (tokens start at zero)."""
+    import numpy as np
+    import workloads
+
+    logits = inputs["logits"]
+    tokens = np.zeros(BATCH * TOKENS * EMBED, np.float32)
+    oracle.broadcast(tokens, inputs["cls"], EMBED, TOKENS * EMBED, BATCH)
+    oracle.add_broadcast(tokens, inputs["pos"], TOKENS * EMBED, BATCH)
+    return {
+        "patches": oracle.extract_patches(inputs["images"], BATCH, CHANNELS, IMAGE, IMAGE, PATCH),
+        "tokens": tokens,
+        "ln_y": oracle.layer_norm(inputs["ln_x"], inputs["gamma"], inputs["beta"], 1e-6),
+        "probabilities": workloads.in_row_chunks(lambda a, b: oracle.softmax(logits[a:b]),
+                                                 SOFTMAX_ROWS, 2048),
+    }
+
+
+class CheckFailed(Exception):
+    """A timed kernel's output differs from the oracle's."""
+
+
+MAX_ABS_FP32 = 1.0e-5
+
+
+def check_first_step(torch, pools, expected) -> dict:
+    """Set 0 after one step against the oracle: gather, class token and
+    positional add bit-exact, LayerNorm and softmax max-abs <= 1e-5."""
+    import numpy as np
+
+    def host(t):
+        return t.cpu().numpy()
+
+    torch.cuda.synchronize()
+    report = {}
+    if not np.array_equal(host(pools.patches[0]).view(np.uint32),
+                          expected["patches"].reshape(-1).view(np.uint32)):
+        raise CheckFailed("patch gather differs from the oracle")
+    if not np.array_equal(host(pools.tokens[0]).view(np.uint32), expected["tokens"].view(np.uint32)):
+        raise CheckFailed("class token / positional add differ from the oracle")
+    for name, got, want in (("layer_norm", pools.ln_y[0], expected["ln_y"]),
+                            ("softmax", pools.logits[0], expected["probabilities"])):
+        got = host(got).reshape(want.shape).astype(np.float64)
+        if not np.isfinite(got).all():
+            raise CheckFailed(f"{name}: non-finite output")
+        worst = float(np.abs(got - want).max())
+        if worst > MAX_ABS_FP32:
+            raise CheckFailed(f"{name}: max-abs error {worst:.3g} > {MAX_ABS_FP32}")
+        report[f"{name}_max_abs"] = float(f"{worst:.3g}")
+    report.update(gather="bit-exact", class_token_positional_add="bit-exact")
+    return report
+
+
+def check_after_timing(torch, pools, expected) -> str:
+    """Every set after the timed steps, on the device: gather outputs bit-exact
+    and LayerNorm outputs within 1e-5 of the oracle (their inputs never
+    change), each image's class-token row equal to cls + pos[0] bit for bit
+    (the broadcast rewrites it every step before the add), every softmax row
+    in [0, 1] and summing to one within 1e-4 (the softmax runs in place, so
+    later steps apply it to probabilities)."""
+    device = pools.gamma.device
+    patches = torch.from_numpy(expected["patches"].reshape(-1)).to(device)
+    ln_y = torch.from_numpy(expected["ln_y"].reshape(-1)).to(device)
+    row0 = torch.from_numpy(expected["tokens"].reshape(BATCH, TOKENS, EMBED)[:, 0, :].copy()).to(device)
+    for i in range(pools.px_sets):
+        if not torch.equal(pools.patches[i].view(torch.int32), patches.view(torch.int32)):
+            raise CheckFailed(f"patch gather set {i} differs after timing")
+    for i in range(pools.ln_sets):
+        worst = float((pools.ln_y[i] - ln_y).abs().max())
+        if not worst <= MAX_ABS_FP32:
+            raise CheckFailed(f"layer_norm set {i}: max-abs error {worst:.3g} after timing")
+    for i in range(pools.tok_sets):
+        got = pools.tokens[i].view(BATCH, TOKENS, EMBED)[:, 0, :]
+        if not torch.equal(got.view(torch.int32), row0.view(torch.int32)):
+            raise CheckFailed(f"class-token rows of token set {i} differ after timing")
+    for i in range(pools.sm_sets):
+        p = pools.logits[i].view(SOFTMAX_ROWS, TOKENS)
+        sums = p.double().sum(dim=1)
+        if not (bool(((p >= 0) & (p <= 1)).all()) and float((sums - 1).abs().max()) <= 1.0e-4):
+            raise CheckFailed(f"softmax set {i}: a row is not a probability vector after timing")
+    torch.cuda.synchronize()
+    return (f"{pools.px_sets} gather, {pools.ln_sets} LayerNorm, {pools.tok_sets} token and "
+            f"{pools.sm_sets} softmax sets checked after timing")
 
 
 def step(launch, i):
@@ -170,15 +282,45 @@ def timed_graph(torch, body, replays: int) -> float:
     return start.elapsed_time(stop) / replays
 
 
+_copier = None
+
+
+def copier():
+    """cuvit_bench_copy from libcuvit_bench.so, the bench-only copy kernel."""
+    global _copier
+    if _copier is None:
+        import ctypes
+
+        path = os.path.join(ROOT, "cu-vit_amd", "lib", "libcuvit_bench.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: build it first (make -C cu-vit_amd)")
+        lib = ctypes.CDLL(path)
+        lib.cuvit_bench_copy.restype = ctypes.c_int
+        lib.cuvit_bench_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                         ctypes.c_void_p]
+        _copier = lib.cuvit_bench_copy
+    return _copier
+
+
 def copy_ceiling(torch, device, nbytes: int) -> float:
-    """ms per device-to-device copy moving the same bytes (half read, half
-    written) over cold rotating buffers: the attainable bound at this size."""
+    """ms per launch of the bench-only copy kernel moving the same bytes (half
+    read, half written) over cold rotating buffers: the attainable bound at
+    this size."""
+    import cuvit_amd
+
     half = nbytes // 2 // 16 * 16
     sets = min(256, max(2, -(-POOL_BYTES // max(nbytes, 1))))
     src = [torch.empty(half, dtype=torch.uint8, device=device) for _ in range(sets)]
     dst = [torch.empty(half, dtype=torch.uint8, device=device) for _ in range(sets)]
-    ms = timed_graph(torch, lambda: [dst[i].copy_(src[i]) for i in range(sets)],
-                     max(1, 200 // sets)) / sets
+    copy = copier()
+
+    def body():
+        stream = cuvit_amd.stream_handle()
+        for i in range(sets):
+            if copy(src[i].data_ptr(), dst[i].data_ptr(), half, stream) != 0:
+                raise RuntimeError("cuvit_bench_copy failed")
+
+    ms = timed_graph(torch, body, max(1, 200 // sets)) / sets
     del src, dst
     return ms
 
@@ -295,29 +437,20 @@ def vit_base_bf16(torch, cuvit, device):
     return results
 
 
-def cpu_baseline(seconds: float):
-    """The CPU oracle over the same workload, one core, until @p seconds of
-    measured work (at least one full step)."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+def cpu_baseline(seconds: float, oracle, inputs):
+    """The CPU oracle over the same workload on the same seeded inputs, one
+    core, whole steps until @p seconds of measured work (at least one step)."""
     import numpy as np
-    from oracle import Oracle
 
-    oracle = Oracle()
-    g = oracle.generator(101)
-    x = g.normal(ROWS * EMBED).reshape(ROWS, EMBED)
-    gamma, beta = g.normal(EMBED, 1.0, 0.02), g.normal(EMBED, 0.0, 0.02)
-    logits = oracle.generator(202).normal(SOFTMAX_ROWS * TOKENS).reshape(SOFTMAX_ROWS, TOKENS)
-    g = oracle.generator(303)
-    images = g.uniform(BATCH * CHANNELS * IMAGE * IMAGE)
-    pos, cls = g.normal(TOKENS * EMBED, 0.0, 0.02), g.normal(EMBED, 0.0, 0.02)
+    x, logits, images = inputs["ln_x"], inputs["logits"], inputs["images"]
     tokens = np.zeros(BATCH * TOKENS * EMBED, np.float32)
     steps, elapsed = 0, 0.0
     while steps == 0 or elapsed < seconds:
         begin = time.perf_counter()
         oracle.extract_patches(images, BATCH, CHANNELS, IMAGE, IMAGE, PATCH)
-        oracle.broadcast(tokens, cls, EMBED, TOKENS * EMBED, BATCH)
-        oracle.add_broadcast(tokens, pos, TOKENS * EMBED, BATCH)
-        oracle.layer_norm(x, gamma, beta, 1e-6)
+        oracle.broadcast(tokens, inputs["cls"], EMBED, TOKENS * EMBED, BATCH)
+        oracle.add_broadcast(tokens, inputs["pos"], TOKENS * EMBED, BATCH)
+        oracle.layer_norm(x, inputs["gamma"], inputs["beta"], 1e-6)
         oracle.softmax(logits)
         elapsed += time.perf_counter() - begin
         steps += 1
@@ -325,8 +458,9 @@ def cpu_baseline(seconds: float):
     return {"value": round(STEP_BYTES / per_step / 1e9, 3), "unit": "GB/s", "cores": 1,
             "kind": "port",
             "sample": f"{steps} full batch-32 steps (gather, cls, pos add, LN [6304,192], "
-                      f"softmax [18912,197]) of the oracle, {elapsed:.1f} s, single thread, "
-                      f"{per_step * 1e3:.1f} ms/step; host has {os.cpu_count()} logical CPUs"}
+                      f"softmax [18912,197]) of the oracle on the GPU leg's seeded inputs, "
+                      f"{elapsed:.1f} s, single thread, {per_step * 1e3:.1f} ms/step; host has "
+                      f"{os.cpu_count()} logical CPUs"}
 
 
 def counters(torch, cuvit, pools):
@@ -427,16 +561,13 @@ def size_sweep(torch, cuvit, device):
             }[name]
             repeats = max(1, 64 // sets)
             ms = timed_graph(torch, lambda: [launch(i) for i in range(sets)], repeats) / sets
-            half = nbytes // 2 // 16 * 16
-            src = [torch.empty(half, dtype=torch.uint8, device=device) for _ in range(sets)]
-            dst = [torch.empty(half, dtype=torch.uint8, device=device) for _ in range(sets)]
-            copy_ms = timed_graph(torch, lambda: [dst[i].copy_(src[i]) for i in range(sets)],
-                                  repeats) / sets
+            del x, y
+            copy_ms = copy_ceiling(torch, device, nbytes)
             gbps = nbytes / (ms * 1e-3) / 1e9
             entry[name] = {"us": round(ms * 1e3, 2), "GBps": round(gbps, 1),
                            "frac_of_peak": round(gbps / HBM_PEAK_GBS, 4),
+                           "copy_us": round(copy_ms * 1e3, 2),
                            "frac_of_copy": round(copy_ms / ms, 3), "MB": round(nbytes / 1e6, 1)}
-            del x, y, src, dst
         results[f"b{batch}"] = entry
     torch.cuda.empty_cache()
     return results
@@ -478,20 +609,29 @@ def main():
 
     cuvit.library()
     device = torch.device("cuda:0")
-    pools = Pools(torch, device)
+    oracle, inputs = seeded_inputs()
+    pools = Pools(torch, device, inputs)
     torch.cuda.synchronize()
     if args.mode == "counters":
         counters(torch, cuvit, pools)
         return
 
     launch = pools.launchers(cuvit)
-    for i in range(args.warmup):
-        step(launch, i)
-    torch.cuda.synchronize()
+    expected = expected_step(oracle, inputs)
+    try:
+        step(launch, 0)
+        checks = check_first_step(torch, pools, expected)
+        for i in range(args.warmup):
+            step(launch, i)
+        torch.cuda.synchronize()
 
-    # K timed steps, one graph, rotating sets.
-    ms_graph = timed_graph(torch, lambda: [step(launch, i) for i in range(args.steps)], 1)
-    ms_per_step = ms_graph / args.steps
+        # K timed steps, one graph, rotating sets.
+        ms_graph = timed_graph(torch, lambda: [step(launch, i) for i in range(args.steps)], 1)
+        ms_per_step = ms_graph / args.steps
+        checks["after_timing"] = check_after_timing(torch, pools, expected)
+    except CheckFailed as failure:
+        print(f"bench.py: output check failed: {failure}", file=sys.stderr, flush=True)
+        sys.exit(3)
 
     # Per-kernel launch durations: back-to-back launches over each pool (cold),
     # and over one set (Infinity-Cache warm).
@@ -531,7 +671,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded device RNG), cold HBM: per-kernel rotating pools > 512 MB",
+        "data": "synthetic: DataGenerator streams (LN seed 101, softmax 202, gather/cls/pos "
+                "303), checked against the oracle before and after timing; cold HBM: per-kernel "
+                "rotating pools > 512 MB",
         "config": {"workload": "ViT-Tiny/16 batch 32: patch gather [32,3,224,224]->[6272,768] + "
                                "class token + positional add into [32,197,192], LayerNorm "
                                "[6304,192], in-place softmax [18912,197]",
@@ -541,6 +683,7 @@ def main():
                      "traffic": measured_traffic().get(dominant),
                      "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT)},
         "kernels": kernels,
+        "checks": checks,
     }
     floor_ms = launch_floor(torch, device)
     step_launches = 5
@@ -575,7 +718,7 @@ def main():
     line["size_sweep"] = size_sweep(torch, cuvit, device)
     line["preprocess"] = preprocess_block(torch, cuvit, device)
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds, oracle, inputs)
     print(json.dumps(line), flush=True)
 
 

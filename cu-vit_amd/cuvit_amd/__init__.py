@@ -268,6 +268,85 @@ def _ptr(x) -> Optional[int]:
     return x.data_ptr()
 
 
+def _operand(x, name: str, dtype: str, elements: int) -> Optional[int]:
+    """The address of operand @p x after checking that the kernel may touch
+    @p elements of it: a torch tensor must live on the GPU, hold @p dtype
+    ("float32", "bfloat16" or "uint8"), be contiguous and have at least that
+    many elements; anything else would be a device access outside the
+    tensor or a host address read by the GPU. Raw int addresses and None go
+    through unchecked, as in the C API (None becomes NULL, which the library
+    rejects with its own message)."""
+    if x is None or isinstance(x, int):
+        return x
+    if x.device.type != "cuda":
+        raise InvalidArgument(ERROR_INVALID_ARGUMENT, f"{name} is not a GPU tensor ({x.device})")
+    if str(x.dtype) != "torch." + dtype:
+        raise InvalidArgument(ERROR_INVALID_ARGUMENT,
+                              f"{name} holds {x.dtype}; this launch needs torch.{dtype}")
+    if not x.is_contiguous():
+        raise InvalidArgument(ERROR_INVALID_ARGUMENT, f"{name} is not contiguous")
+    if x.numel() < elements:
+        raise InvalidArgument(ERROR_INVALID_ARGUMENT,
+                              f"{name} holds {x.numel()} elements; the launch touches {elements}")
+    return x.data_ptr()
+
+
+def _positive(*extents) -> bool:
+    """True when every extent is positive: only then are the operand checks
+    applied, so that zero and negative extents reach the library's own
+    checks in the reference's order (a zero extent returns first, even with
+    null pointers; a negative one is InvalidArgument)."""
+    return all(int(e) > 0 for e in extents)
+
+
+def _storage(bf16: bool) -> str:
+    return "bfloat16" if bf16 else "float32"
+
+
+def _offset_range(count: int, inner: int, stride: int, outer_stride: int):
+    """Smallest and largest element offset of a batch entry's operand
+    (split batches: entry i sits at (i / inner) * outer_stride + (i % inner)
+    * stride; flat ones at i * stride)."""
+    if 0 < inner < count:
+        outer_span = (count // inner - 1) * outer_stride
+        inner_span = (inner - 1) * stride
+        return (min(0, outer_span) + min(0, inner_span), max(0, outer_span) + max(0, inner_span))
+    span = (count - 1) * stride
+    return min(0, span), max(0, span)
+
+
+def _gemm_operands(a, b, bias, c, problem: "GemmProblem", bf16: bool):
+    p = problem
+    if not _positive(p.m, p.n, p.batch.count) or p.k < 0:
+        return _ptr(a), _ptr(b), _ptr(bias), _ptr(c)
+    transposed = p.layout == TRANSPOSED
+    lda = p.lda or p.k
+    ldb = p.ldb or (p.k if transposed else p.n)
+    ldc = p.ldc or p.n
+    if lda < p.k or ldc < p.n or ldb < (p.k if transposed else p.n):
+        return _ptr(a), _ptr(b), _ptr(bias), _ptr(c)  # the library names the bad ld
+    count, inner = p.batch.count, p.batch.inner
+
+    def span(rows: int, ld: int, cols: int, stride: int, outer_stride: int, name: str) -> int:
+        if rows <= 0 or cols <= 0:
+            return 0
+        low, high = _offset_range(count, inner, stride, outer_stride)
+        if low < 0:
+            raise InvalidArgument(ERROR_INVALID_ARGUMENT,
+                                  f"{name}: a batch entry starts before the tensor")
+        return high + (rows - 1) * ld + cols
+
+    t = _storage(bf16)
+    a_rows, a_cols = p.m, p.k
+    b_rows, b_cols = (p.n, p.k) if transposed else (p.k, p.n)
+    return (_operand(a, "A", t, span(a_rows, lda, a_cols, p.batch.stride_a,
+                                     p.batch.outer_stride_a, "A")),
+            _operand(b, "B", t, span(b_rows, ldb, b_cols, p.batch.stride_b,
+                                     p.batch.outer_stride_b, "B")),
+            _operand(bias, "bias", "float32", p.n),
+            _operand(c, "C", t, span(p.m, ldc, p.n, p.batch.stride_c, p.batch.outer_stride_c, "C")))
+
+
 def stream_handle(stream=None) -> Optional[int]:
     """hipStream_t of a torch stream (default: torch's current stream)."""
     import torch
@@ -295,59 +374,92 @@ def gemm_problem(m: int, n: int, k: int, layout: int = NO_TRANSPOSE) -> GemmProb
 
 
 def gemm(a, b, bias, c, problem: GemmProblem, stream=None, bf16: Optional[bool] = None) -> None:
-    fn = library().cuvit_gemm_bf16 if (bf16 if bf16 is not None else _bf16(a)) else library().cuvit_gemm_f32
-    check(fn(_ptr(a), _ptr(b), _ptr(bias), _ptr(c), ctypes.byref(problem), stream_handle(stream)))
+    bf16 = bf16 if bf16 is not None else _bf16(a)
+    fn = library().cuvit_gemm_bf16 if bf16 else library().cuvit_gemm_f32
+    pa, pb, pbias, pc = _gemm_operands(a, b, bias, c, problem, bf16)
+    check(fn(pa, pb, pbias, pc, ctypes.byref(problem), stream_handle(stream)))
 
 
 def layer_norm(x, gamma, beta, out, rows: int, columns: int, epsilon: float = 1.0e-6,
                stream=None, bf16: Optional[bool] = None) -> None:
-    fn = library().cuvit_layer_norm_bf16 if (bf16 if bf16 is not None else _bf16(x)) else library().cuvit_layer_norm_f32
+    bf16 = bf16 if bf16 is not None else _bf16(x)
+    fn = library().cuvit_layer_norm_bf16 if bf16 else library().cuvit_layer_norm_f32
+    if _positive(rows, columns):
+        t, n = _storage(bf16), rows * columns
+        x, out = _operand(x, "x", t, n), _operand(out, "out", t, n)
+        gamma = _operand(gamma, "gamma", "float32", columns)
+        beta = _operand(beta, "beta", "float32", columns)
     check(fn(_ptr(x), _ptr(gamma), _ptr(beta), _ptr(out), rows, columns, epsilon,
              stream_handle(stream)))
 
 
 def softmax(x, out, rows: int, columns: int, stream=None, bf16: Optional[bool] = None) -> None:
-    fn = library().cuvit_softmax_bf16 if (bf16 if bf16 is not None else _bf16(x)) else library().cuvit_softmax_f32
+    bf16 = bf16 if bf16 is not None else _bf16(x)
+    fn = library().cuvit_softmax_bf16 if bf16 else library().cuvit_softmax_f32
+    if _positive(rows, columns):
+        t, n = _storage(bf16), rows * columns
+        x, out = _operand(x, "x", t, n), _operand(out, "out", t, n)
     check(fn(_ptr(x), _ptr(out), rows, columns, stream_handle(stream)))
 
 
 def gelu(x, out, count: int, stream=None, bf16: Optional[bool] = None) -> None:
-    fn = library().cuvit_gelu_bf16 if (bf16 if bf16 is not None else _bf16(x)) else library().cuvit_gelu_f32
+    bf16 = bf16 if bf16 is not None else _bf16(x)
+    fn = library().cuvit_gelu_bf16 if bf16 else library().cuvit_gelu_f32
+    if _positive(count):
+        x, out = _operand(x, "x", _storage(bf16), count), _operand(out, "out", _storage(bf16), count)
     check(fn(_ptr(x), _ptr(out), count, stream_handle(stream)))
 
 
 def extract_patches(images, patches, batch: int, channels: int, height: int, width: int,
                     patch: int, stream=None, bf16: Optional[bool] = None) -> None:
-    fn = (library().cuvit_extract_patches_bf16 if (bf16 if bf16 is not None else _bf16(images))
-          else library().cuvit_extract_patches_f32)
+    bf16 = bf16 if bf16 is not None else _bf16(images)
+    fn = library().cuvit_extract_patches_bf16 if bf16 else library().cuvit_extract_patches_f32
+    if _positive(batch, channels, height, width, patch):
+        n = batch * channels * height * width
+        images = _operand(images, "images", _storage(bf16), n)
+        patches = _operand(patches, "patches", _storage(bf16), n)
     check(fn(_ptr(images), _ptr(patches), batch, channels, height, width, patch,
              stream_handle(stream)))
 
 
 def add(accumulator, addend, count: int, stream=None) -> None:
+    if _positive(count):
+        accumulator = _operand(accumulator, "accumulator", "float32", count)
+        addend = _operand(addend, "addend", "float32", count)
     check(library().cuvit_add_f32(_ptr(accumulator), _ptr(addend), count, stream_handle(stream)))
 
 
 def add_broadcast(accumulator, addend, count: int, batch: int, stream=None) -> None:
+    if _positive(count, batch):
+        accumulator = _operand(accumulator, "accumulator", "float32", count * batch)
+        addend = _operand(addend, "addend", "float32", count)
     check(library().cuvit_add_broadcast_f32(_ptr(accumulator), _ptr(addend), count, batch,
                                             stream_handle(stream)))
 
 
 def broadcast(destination, source, count: int, destination_stride: int, batch: int,
               stream=None, bf16: Optional[bool] = None) -> None:
-    fn = (library().cuvit_broadcast_bf16 if (bf16 if bf16 is not None else _bf16(destination))
-          else library().cuvit_broadcast_f32)
+    bf16 = bf16 if bf16 is not None else _bf16(destination)
+    fn = library().cuvit_broadcast_bf16 if bf16 else library().cuvit_broadcast_f32
+    if _positive(count, batch) and destination_stride >= count:
+        destination = _operand(destination, "destination", _storage(bf16),
+                               (batch - 1) * destination_stride + count)
+        source = _operand(source, "source", _storage(bf16), count)
     check(fn(_ptr(destination), _ptr(source), count, destination_stride, batch,
              stream_handle(stream)))
 
 
 def convert_to_bf16(x, out, count: int, stream=None) -> None:
     """fp32 -> bf16, round to nearest-even (an extension)."""
+    if _positive(count):
+        x, out = _operand(x, "x", "float32", count), _operand(out, "out", "bfloat16", count)
     check(library().cuvit_convert_f32_to_bf16(_ptr(x), _ptr(out), count, stream_handle(stream)))
 
 
 def convert_to_f32(x, out, count: int, stream=None) -> None:
     """bf16 -> fp32, exact (an extension)."""
+    if _positive(count):
+        x, out = _operand(x, "x", "bfloat16", count), _operand(out, "out", "float32", count)
     check(library().cuvit_convert_bf16_to_f32(_ptr(x), _ptr(out), count, stream_handle(stream)))
 
 
@@ -362,7 +474,12 @@ def attention(qkv, context, images: int, heads: int, tokens: int, head_dim: int,
     [images, tokens, 3, heads, head_dim] projection into
     [images, tokens, heads, head_dim]; an extension replacing the reference's
     three attention launches (vit.cu:205-245) with bitwise the same result."""
-    fn = library().cuvit_attention_bf16 if _bf16(qkv) else library().cuvit_attention_f32
+    bf16 = _bf16(qkv)
+    fn = library().cuvit_attention_bf16 if bf16 else library().cuvit_attention_f32
+    if _positive(images, heads, tokens, head_dim):
+        n = images * tokens * heads * head_dim
+        qkv = _operand(qkv, "qkv", _storage(bf16), 3 * n)
+        context = _operand(context, "context", _storage(bf16), n)
     check(fn(_ptr(qkv), _ptr(context), images, heads, tokens, head_dim, stream_handle(stream)))
 
 
@@ -496,6 +613,11 @@ class VisionTransformer:
         return library().cuvit_vit_precision(self._handle)
 
     def forward(self, images, logits, batch: int, stream=None) -> None:
+        c = self.config
+        if _positive(batch):
+            images = _operand(images, "images", "float32",
+                              batch * c.channels * c.image_size * c.image_size)
+            logits = _operand(logits, "logits", "float32", batch * c.classes)
         check(library().cuvit_vit_forward(self._handle, _ptr(images), _ptr(logits), batch,
                                           stream_handle(stream)))
 
@@ -570,6 +692,9 @@ def preprocess(pixels, tensor, batch: int, width: int, height: int,
     uint8 into the device tensor [batch, 3, size, size] float (the reference's
     preprocess, image.cpp:95-135, batched on the GPU)."""
     settings = settings if settings is not None else Preprocessing()
+    if _positive(batch, width, height, settings.size):
+        pixels = _operand(pixels, "pixels", "uint8", batch * height * width * 3)
+        tensor = _operand(tensor, "tensor", "float32", batch * 3 * settings.size * settings.size)
     check(library().cuvit_preprocess_u8(_ptr(pixels), batch, width, height,
                                         ctypes.byref(settings), _ptr(tensor),
                                         stream_handle(stream)))

@@ -272,3 +272,40 @@ def test_last_error_belongs_to_the_calling_thread(cuvit):
     for thread in threads:
         thread.join()
     assert not failures, failures[:3]
+
+
+def test_host_tensors_are_refused_before_any_launch(cuvit):
+    """A torch tensor in host memory never reaches a kernel as a device address:
+    the binding names the operand and raises InvalidArgument. Zero and negative
+    extents still go to the library's own checks first."""
+    import torch
+
+    x = torch.zeros(4 * 8)
+    g = torch.ones(8)
+    with pytest.raises(cuvit.InvalidArgument, match="x is not a GPU tensor"):
+        cuvit.layer_norm(x, g, g, FAKE, 4, 8)
+    with pytest.raises(cuvit.InvalidArgument, match="out is not a GPU tensor"):
+        cuvit.softmax(FAKE, x, 4, 8)
+    with pytest.raises(cuvit.InvalidArgument, match="images is not a GPU tensor"):
+        cuvit.extract_patches(torch.zeros(3 * 16 * 16), FAKE, 1, 3, 16, 16, 8)
+    with pytest.raises(cuvit.InvalidArgument, match="A is not a GPU tensor"):
+        cuvit.gemm(torch.zeros(12), FAKE, None, FAKE, cuvit.gemm_problem(3, 4, 4))
+    with pytest.raises(cuvit.InvalidArgument, match="pixels is not a GPU tensor"):
+        cuvit.preprocess(torch.zeros(4 * 4 * 3, dtype=torch.uint8), FAKE, 1, 4, 4,
+                         cuvit.Preprocessing(size=4))
+    # The library's order still holds where an extent is zero or negative.
+    cuvit.layer_norm(x, g, g, x, 0, 8)
+    with pytest.raises(cuvit.InvalidArgument, match="cannot be negative"):
+        cuvit.gelu(x, x, -5)
+
+
+def test_gemm_operand_spans_follow_the_batch_layout(cuvit):
+    """The elements a GEMM touches per operand, which the binding requires each
+    tensor to hold: the last batch entry's offset plus its last row."""
+    from cuvit_amd import _offset_range
+
+    assert _offset_range(1, 0, 100, 0) == (0, 0)
+    assert _offset_range(4, 0, 100, 0) == (0, 300)
+    assert _offset_range(6, 3, 10, 1000) == (0, 1000 + 20)    # 2 outer groups of 3
+    assert _offset_range(6, 6, 10, 1000) == (0, 50)           # one group: flat
+    assert _offset_range(4, 0, -5, 0) == (-15, 0)

@@ -14,6 +14,7 @@ import numpy as np
 import pytest
 import torch
 
+import workloads as W
 from conftest import to_device, to_host
 from numerics import TestFailure, compare_close, require_close, require_close_scaled, \
     require_exact
@@ -294,25 +295,25 @@ def test_zero_k_produces_the_bias(cuvit, oracle, device):
     ("fc2 accumulate b32", 6304, 192, 768, False, True),
 ])
 def test_vit_tiny_batch_32_epilogue_gemms(cuvit, oracle, device, name, m, n, k, gelu, accumulate):
-    """The C4 epilogue carriers at full size, judged on a row sample against the
-    oracle (term-scaled, and GELU's elementwise tolerance after it)."""
+    """The C4 epilogue carriers at full size, every row judged against the
+    oracle (term-scaled, and GELU's elementwise tolerance after it). Outputs
+    that are not accumulated into start as NaN, so an unwritten tile fails."""
     g = oracle.generator(404 + m + n + k)
     a = g.normal(m * k)
     w = g.normal(n * k, 0.0, 0.02)
     bias = g.normal(n, 0.0, 0.02)
-    existing = g.normal(m * n)
+    existing = g.normal(m * n) if accumulate else np.full(m * n, np.nan, np.float32)
     dc = to_device(existing, device)
     problem = cuvit.gemm_problem(m, n, k, T)
     problem.epilogue.gelu = int(gelu)
     problem.epilogue.accumulate = int(accumulate)
     cuvit.gemm(to_device(a, device), to_device(w, device), to_device(bias, device), dc, problem)
     actual = to_host(dc).reshape(m, n)
-    rows = np.r_[0:64, m // 2:m // 2 + 64, m - 64:m]
-    sample_a = a.reshape(m, k)[rows]
-    pre = oracle.gemm_transposed(sample_a, w, bias, rows.size, n, k)
-    scale = oracle.term_magnitudes(sample_a, w, rows.size, n, k, True)
+    a = a.reshape(m, k)
+    pre = W.in_row_chunks(lambda s, e: oracle.gemm_transposed(a[s:e], w, bias, e - s, n, k), m, 256)
+    scale = W.in_row_chunks(lambda s, e: oracle.term_magnitudes(a[s:e], w, e - s, n, k, True), m, 256)
     if gelu:
-        require_close(actual[rows], oracle.gelu(pre), name, 1.0e-4, 1.0e-5)
+        require_close(actual, oracle.gelu(pre), name, 1.0e-4, 1.0e-5)
     else:
-        expected = existing.reshape(m, n)[rows] + pre if accumulate else pre
-        require_close_scaled(actual[rows], expected, scale, name, 1.0e-6, 1.0e-5)
+        expected = existing.reshape(m, n) + pre if accumulate else pre
+        require_close_scaled(actual, expected, scale, name, 1.0e-6, 1.0e-5)
