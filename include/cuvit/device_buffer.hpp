@@ -1,16 +1,23 @@
 #pragma once
 
-// Owner of one device allocation, the counterpart of the reference's
-// DeviceBuffer<T> (include/cuvit/device_buffer.hpp:22-244): move-only, records
-// the device it lives on, synchronous and stream-ordered copies with bounds
-// checks, rejects cross-device and overlapping self copies, zero fills.
+// One device allocation owned by one object. Interface of the reference's
+// DeviceBuffer<T> (include/cuvit/device_buffer.hpp:22-244): an element count,
+// allocate / reset, blocking and stream-ordered copies to and from the host
+// and between buffers of one device, zero fills, moves, and the device the
+// memory lives on.
+//
+// The allocation sits in a unique_ptr whose deleter remembers the owning
+// device and makes it current for hipFree. Every copy goes through one routine
+// that checks the element range first, then skips empty copies, then checks
+// the other side (a host pointer, or a device buffer: same device, and for a
+// copy within one buffer, ranges that do not overlap).
 
 #include "cuvit/hip_check.hpp"
 
 #include <hip/hip_runtime_api.h>
 
 #include <cstddef>
-#include <limits>
+#include <memory>
 #include <stdexcept>
 #include <string>
 #include <type_traits>
@@ -19,182 +26,181 @@
 namespace cuvit {
 
 template <typename T> class DeviceBuffer final {
-    static_assert(!std::is_const<T>::value, "DeviceBuffer cannot own const elements");
-    static_assert(!std::is_reference<T>::value, "DeviceBuffer cannot own references");
-    static_assert(std::is_trivially_copyable<T>::value,
-                  "DeviceBuffer elements must be trivially copyable");
+    static_assert(std::is_trivially_copyable<T>::value && !std::is_const<T>::value &&
+                      !std::is_reference<T>::value,
+                  "DeviceBuffer holds mutable, trivially copyable elements");
 
   public:
     DeviceBuffer() noexcept = default;
     explicit DeviceBuffer(std::size_t count) { allocate(count); }
-    ~DeviceBuffer() { release(); }
 
-    DeviceBuffer(const DeviceBuffer&) = delete;
-    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    DeviceBuffer(DeviceBuffer&& other) noexcept
+        : memory_(std::move(other.memory_)), count_(std::exchange(other.count_, 0)) {}
 
-    DeviceBuffer(DeviceBuffer&& other) noexcept { swap(other); }
     DeviceBuffer& operator=(DeviceBuffer&& other) noexcept {
-        if (this != &other) {
-            release();
-            swap(other);
-        }
+        DeviceBuffer(std::move(other)).swap(*this);
         return *this;
     }
 
-    /// Owns exactly @p count elements on the current device. Asking for the
-    /// size already held keeps the allocation, its contents and its device.
+    /// Holds exactly @p count elements on the current device afterwards. The
+    /// count already held changes nothing (memory, contents and device stay);
+    /// any other count replaces the allocation, zero releases it.
     void allocate(std::size_t count) {
-        if (count == size_) {
-            return;
+        if (count != count_) {
+            DeviceBuffer(Sized{}, count).swap(*this);
         }
-        DeviceBuffer fresh;
-        if (count != 0) {
-            CUVIT_HIP_CHECK(hipGetDevice(&fresh.device_));
-            void* memory = nullptr;
-            CUVIT_HIP_CHECK(hipMalloc(&memory, byte_count(count)));
-            fresh.data_ = static_cast<T*>(memory);
-            fresh.size_ = count;
-        }
-        swap(fresh);
     }
 
-    void reset() noexcept { release(); }
+    void reset() noexcept { DeviceBuffer().swap(*this); }
 
     void copy_from_host(const T* source, std::size_t count, std::size_t offset = 0) {
-        if (prepare(count, offset, source, "source")) {
-            CUVIT_HIP_CHECK(hipMemcpy(data_ + offset, source, byte_count(count), hipMemcpyHostToDevice));
-        }
+        from_host(source, count, offset, nullptr);
     }
-
     void copy_from_host_async(const T* source, std::size_t count, hipStream_t stream,
                               std::size_t offset = 0) {
-        if (prepare(count, offset, source, "source")) {
-            CUVIT_HIP_CHECK(hipMemcpyAsync(data_ + offset, source, byte_count(count),
-                                           hipMemcpyHostToDevice, stream));
-        }
+        from_host(source, count, offset, &stream);
     }
-
     void copy_to_host(T* destination, std::size_t count, std::size_t offset = 0) const {
-        if (prepare(count, offset, destination, "destination")) {
-            CUVIT_HIP_CHECK(hipMemcpy(destination, data_ + offset, byte_count(count), hipMemcpyDeviceToHost));
-        }
+        to_host(destination, count, offset, nullptr);
     }
-
     void copy_to_host_async(T* destination, std::size_t count, hipStream_t stream,
                             std::size_t offset = 0) const {
-        if (prepare(count, offset, destination, "destination")) {
-            CUVIT_HIP_CHECK(hipMemcpyAsync(destination, data_ + offset, byte_count(count),
-                                           hipMemcpyDeviceToHost, stream));
-        }
+        to_host(destination, count, offset, &stream);
     }
-
     void copy_from_device(const DeviceBuffer& source, std::size_t count,
                           std::size_t source_offset = 0, std::size_t destination_offset = 0) {
-        if (prepare_device(source, count, source_offset, destination_offset)) {
-            CUVIT_HIP_CHECK(hipMemcpy(data_ + destination_offset, source.data_ + source_offset,
-                                      byte_count(count), hipMemcpyDeviceToDevice));
-        }
+        from_device(source, count, source_offset, destination_offset, nullptr);
     }
-
     void copy_from_device_async(const DeviceBuffer& source, std::size_t count, hipStream_t stream,
                                 std::size_t source_offset = 0, std::size_t destination_offset = 0) {
-        if (prepare_device(source, count, source_offset, destination_offset)) {
-            CUVIT_HIP_CHECK(hipMemcpyAsync(data_ + destination_offset, source.data_ + source_offset,
-                                           byte_count(count), hipMemcpyDeviceToDevice, stream));
-        }
+        from_device(source, count, source_offset, destination_offset, &stream);
     }
 
     void fill_zero() {
-        if (!empty()) {
-            CUVIT_HIP_CHECK(hipMemset(data_, 0, bytes()));
+        if (count_ != 0) {
+            CUVIT_HIP_CHECK(hipMemset(data(), 0, bytes()));
         }
     }
-
     void fill_zero_async(hipStream_t stream) {
-        if (!empty()) {
-            CUVIT_HIP_CHECK(hipMemsetAsync(data_, 0, bytes(), stream));
+        if (count_ != 0) {
+            CUVIT_HIP_CHECK(hipMemsetAsync(data(), 0, bytes(), stream));
         }
     }
 
     void swap(DeviceBuffer& other) noexcept {
-        std::swap(data_, other.data_);
-        std::swap(size_, other.size_);
-        std::swap(device_, other.device_);
+        memory_.swap(other.memory_);
+        std::swap(count_, other.count_);
     }
 
-    [[nodiscard]] T* data() noexcept { return data_; }
-    [[nodiscard]] const T* data() const noexcept { return data_; }
-    [[nodiscard]] std::size_t size() const noexcept { return size_; }
-    [[nodiscard]] std::size_t bytes() const noexcept { return size_ * sizeof(T); }
-    [[nodiscard]] bool empty() const noexcept { return size_ == 0; }
-    /// Device holding the allocation, or -1 when empty.
-    [[nodiscard]] int device() const noexcept { return device_; }
+    [[nodiscard]] T* data() noexcept { return memory_.get(); }
+    [[nodiscard]] const T* data() const noexcept { return memory_.get(); }
+    [[nodiscard]] std::size_t size() const noexcept { return count_; }
+    [[nodiscard]] std::size_t bytes() const noexcept { return count_ * sizeof(T); }
+    [[nodiscard]] bool empty() const noexcept { return count_ == 0; }
+    /// The device holding the memory; -1 when there is none.
+    [[nodiscard]] int device() const noexcept {
+        return memory_ ? memory_.get_deleter().device : -1;
+    }
 
   private:
-    static std::size_t byte_count(std::size_t count) {
-        if (count > std::numeric_limits<std::size_t>::max() / sizeof(T)) {
-            throw std::overflow_error("DeviceBuffer byte size overflow");
-        }
-        return count * sizeof(T);
-    }
-
-    void check_range(std::size_t count, std::size_t offset) const {
-        if (offset > size_ || count > size_ - offset) {
-            throw std::out_of_range("DeviceBuffer copy exceeds allocation bounds");
-        }
-    }
-
-    /// Validates a host copy; false when there is nothing to copy.
-    bool prepare(std::size_t count, std::size_t offset, const void* host, const char* role) const {
-        check_range(count, offset);
-        if (count == 0) {
-            return false;
-        }
-        if (host == nullptr) {
-            throw std::invalid_argument(std::string("Host ") + role + " pointer cannot be null");
-        }
-        return true;
-    }
-
-    bool prepare_device(const DeviceBuffer& source, std::size_t count, std::size_t source_offset,
-                        std::size_t destination_offset) const {
-        source.check_range(count, source_offset);
-        check_range(count, destination_offset);
-        if (count == 0) {
-            return false;
-        }
-        if (source.device_ != device_) {
-            throw std::invalid_argument("DeviceBuffer copies between different devices are not supported");
-        }
-        if (this == &source) {
-            const std::size_t gap = source_offset > destination_offset ? source_offset - destination_offset
-                                                                       : destination_offset - source_offset;
-            if (gap < count) {
-                throw std::invalid_argument("DeviceBuffer device-to-device copy ranges must not overlap");
-            }
-        }
-        return true;
-    }
-
-    void release() noexcept {
-        if (data_ != nullptr) {
-            // hipFree wants the owning device current.
+    struct FreeOnDevice {
+        int device = -1;
+        void operator()(T* memory) const noexcept {
             int current = -1;
-            const bool switched = hipGetDevice(&current) == hipSuccess && current != device_ &&
-                                  hipSetDevice(device_) == hipSuccess;
-            static_cast<void>(hipFree(data_));
-            if (switched) {
+            const bool away = hipGetDevice(&current) == hipSuccess && current != device;
+            if (away) {
+                static_cast<void>(hipSetDevice(device));
+            }
+            static_cast<void>(hipFree(memory));
+            if (away) {
                 static_cast<void>(hipSetDevice(current));
             }
         }
-        data_ = nullptr;
-        size_ = 0;
-        device_ = -1;
+    };
+    struct Sized {};
+
+    DeviceBuffer(Sized, std::size_t count) : count_(count) {
+        if (count == 0) {
+            return;
+        }
+        int device = -1;
+        CUVIT_HIP_CHECK(hipGetDevice(&device));
+        void* memory = nullptr;
+        CUVIT_HIP_CHECK(hipMalloc(&memory, byte_count(count)));
+        memory_ = Memory(static_cast<T*>(memory), FreeOnDevice{device});
     }
 
-    T* data_ = nullptr;
-    std::size_t size_ = 0;
-    int device_ = -1;
+    static std::size_t byte_count(std::size_t count) {
+        std::size_t total = 0;
+        if (__builtin_mul_overflow(count, sizeof(T), &total)) {
+            throw std::overflow_error("DeviceBuffer byte size overflow");
+        }
+        return total;
+    }
+
+    /// Whether [offset, offset + count) lies inside the buffer; throws if not.
+    void require_range(std::size_t count, std::size_t offset) const {
+        if (offset <= count_ && count <= count_ - offset) {
+            return;
+        }
+        throw std::out_of_range("DeviceBuffer copy of " + std::to_string(count) +
+                                " elements at offset " + std::to_string(offset) +
+                                " leaves the allocation of " + std::to_string(count_));
+    }
+
+    static void move_bytes(void* to, const void* from, std::size_t bytes, hipMemcpyKind kind,
+                           const hipStream_t* stream) {
+        if (stream != nullptr) {
+            CUVIT_HIP_CHECK(hipMemcpyAsync(to, from, bytes, kind, *stream));
+        } else {
+            CUVIT_HIP_CHECK(hipMemcpy(to, from, bytes, kind));
+        }
+    }
+
+    void from_host(const T* source, std::size_t count, std::size_t offset, const hipStream_t* stream) {
+        require_range(count, offset);
+        if (count == 0) {
+            return;
+        }
+        if (source == nullptr) {
+            throw std::invalid_argument("DeviceBuffer copy: the host source is null");
+        }
+        move_bytes(data() + offset, source, count * sizeof(T), hipMemcpyHostToDevice, stream);
+    }
+
+    void to_host(T* destination, std::size_t count, std::size_t offset, const hipStream_t* stream) const {
+        require_range(count, offset);
+        if (count == 0) {
+            return;
+        }
+        if (destination == nullptr) {
+            throw std::invalid_argument("DeviceBuffer copy: the host destination is null");
+        }
+        move_bytes(destination, data() + offset, count * sizeof(T), hipMemcpyDeviceToHost, stream);
+    }
+
+    void from_device(const DeviceBuffer& source, std::size_t count, std::size_t source_offset,
+                     std::size_t destination_offset, const hipStream_t* stream) {
+        source.require_range(count, source_offset);
+        require_range(count, destination_offset);
+        if (count == 0) {
+            return;
+        }
+        if (source.device() != device()) {
+            throw std::invalid_argument("DeviceBuffer copy: the buffers live on different devices");
+        }
+        const bool overlapping = &source == this && (source_offset < destination_offset + count &&
+                                                     destination_offset < source_offset + count);
+        if (overlapping) {
+            throw std::invalid_argument("DeviceBuffer copy: source and destination ranges overlap");
+        }
+        move_bytes(data() + destination_offset, source.data() + source_offset, count * sizeof(T),
+                   hipMemcpyDeviceToDevice, stream);
+    }
+
+    using Memory = std::unique_ptr<T, FreeOnDevice>;
+    Memory memory_;
+    std::size_t count_ = 0;
 };
 
 template <typename T> void swap(DeviceBuffer<T>& left, DeviceBuffer<T>& right) noexcept {

@@ -1,9 +1,13 @@
 #pragma once
 
-// Owner of pinned host memory, the counterpart of the reference's HostBuffer<T>
-// (include/cuvit/host_buffer.hpp:25-134). Memory comes from hipHostMalloc, so
-// stream-ordered copies from it are truly asynchronous. Allocate once and reuse:
-// pinning is expensive.
+// Page-locked host memory owned by one object. Interface of the reference's
+// HostBuffer<T> (include/cuvit/host_buffer.hpp:25-134): an element count,
+// allocate / reset, indexed and checked access, iteration, zero fill, moves.
+// Pinned pages make stream-ordered copies from and to them asynchronous, and
+// pinning is slow, so a buffer is meant to be sized once and reused.
+//
+// The pages sit in a unique_ptr whose deleter returns them with hipHostFree;
+// the element count travels beside it.
 
 #include "cuvit/hip_check.hpp"
 
@@ -11,7 +15,7 @@
 
 #include <cstddef>
 #include <cstring>
-#include <limits>
+#include <memory>
 #include <stdexcept>
 #include <type_traits>
 #include <utility>
@@ -19,96 +23,88 @@
 namespace cuvit {
 
 template <typename T> class HostBuffer final {
-    static_assert(!std::is_const<T>::value, "HostBuffer cannot own const elements");
-    static_assert(!std::is_reference<T>::value, "HostBuffer cannot own references");
-    static_assert(std::is_trivially_copyable<T>::value,
-                  "HostBuffer elements must be trivially copyable");
+    static_assert(std::is_trivially_copyable<T>::value && !std::is_const<T>::value &&
+                      !std::is_reference<T>::value,
+                  "HostBuffer holds mutable, trivially copyable elements");
 
   public:
     HostBuffer() noexcept = default;
     explicit HostBuffer(std::size_t count) { allocate(count); }
-    ~HostBuffer() { release(); }
 
-    HostBuffer(const HostBuffer&) = delete;
-    HostBuffer& operator=(const HostBuffer&) = delete;
+    HostBuffer(HostBuffer&& other) noexcept
+        : pages_(std::move(other.pages_)), count_(std::exchange(other.count_, 0)) {}
 
-    HostBuffer(HostBuffer&& other) noexcept { swap(other); }
     HostBuffer& operator=(HostBuffer&& other) noexcept {
-        if (this != &other) {
-            release();
-            swap(other);
-        }
+        HostBuffer(std::move(other)).swap(*this);
         return *this;
     }
 
-    /// Owns exactly @p count pinned elements; the current size is a no-op.
+    /// Holds exactly @p count elements afterwards. The count already held
+    /// changes nothing, so the contents survive; any other count replaces
+    /// the pages (contents not kept), zero releases them.
     void allocate(std::size_t count) {
-        if (count == size_) {
-            return;
+        if (count != count_) {
+            HostBuffer(Sized{}, count).swap(*this);
         }
-        HostBuffer fresh;
-        if (count != 0) {
-            if (count > std::numeric_limits<std::size_t>::max() / sizeof(T)) {
-                throw std::overflow_error("HostBuffer byte size overflow");
-            }
-            void* memory = nullptr;
-            CUVIT_HIP_CHECK(hipHostMalloc(&memory, count * sizeof(T), hipHostMallocDefault));
-            fresh.data_ = static_cast<T*>(memory);
-            fresh.size_ = count;
-        }
-        swap(fresh);
     }
 
-    void reset() noexcept { release(); }
+    void reset() noexcept { HostBuffer().swap(*this); }
 
     void fill_zero() noexcept {
-        if (data_ != nullptr) {
-            std::memset(static_cast<void*>(data_), 0, bytes());
+        if (count_ != 0) {
+            std::memset(static_cast<void*>(pages_.get()), 0, bytes());
         }
     }
 
     void swap(HostBuffer& other) noexcept {
-        std::swap(data_, other.data_);
-        std::swap(size_, other.size_);
+        pages_.swap(other.pages_);
+        std::swap(count_, other.count_);
     }
 
-    [[nodiscard]] T& operator[](std::size_t index) noexcept { return data_[index]; }
-    [[nodiscard]] const T& operator[](std::size_t index) const noexcept { return data_[index]; }
+    [[nodiscard]] T& operator[](std::size_t i) noexcept { return pages_.get()[i]; }
+    [[nodiscard]] const T& operator[](std::size_t i) const noexcept { return pages_.get()[i]; }
 
-    [[nodiscard]] T& at(std::size_t index) {
-        if (index >= size_) {
-            throw std::out_of_range("HostBuffer index is out of range");
-        }
-        return data_[index];
-    }
-    [[nodiscard]] const T& at(std::size_t index) const {
-        if (index >= size_) {
-            throw std::out_of_range("HostBuffer index is out of range");
-        }
-        return data_[index];
-    }
+    [[nodiscard]] T& at(std::size_t i) { return pages_.get()[checked(i)]; }
+    [[nodiscard]] const T& at(std::size_t i) const { return pages_.get()[checked(i)]; }
 
-    [[nodiscard]] T* data() noexcept { return data_; }
-    [[nodiscard]] const T* data() const noexcept { return data_; }
-    [[nodiscard]] T* begin() noexcept { return data_; }
-    [[nodiscard]] const T* begin() const noexcept { return data_; }
-    [[nodiscard]] T* end() noexcept { return data_ + size_; }
-    [[nodiscard]] const T* end() const noexcept { return data_ + size_; }
-    [[nodiscard]] std::size_t size() const noexcept { return size_; }
-    [[nodiscard]] std::size_t bytes() const noexcept { return size_ * sizeof(T); }
-    [[nodiscard]] bool empty() const noexcept { return size_ == 0; }
+    [[nodiscard]] T* data() noexcept { return pages_.get(); }
+    [[nodiscard]] const T* data() const noexcept { return pages_.get(); }
+    [[nodiscard]] T* begin() noexcept { return data(); }
+    [[nodiscard]] const T* begin() const noexcept { return data(); }
+    [[nodiscard]] T* end() noexcept { return data() + count_; }
+    [[nodiscard]] const T* end() const noexcept { return data() + count_; }
+    [[nodiscard]] std::size_t size() const noexcept { return count_; }
+    [[nodiscard]] std::size_t bytes() const noexcept { return count_ * sizeof(T); }
+    [[nodiscard]] bool empty() const noexcept { return count_ == 0; }
 
   private:
-    void release() noexcept {
-        if (data_ != nullptr) {
-            static_cast<void>(hipHostFree(data_));
+    struct Unpin {
+        void operator()(T* pages) const noexcept { static_cast<void>(hipHostFree(pages)); }
+    };
+    struct Sized {};
+
+    HostBuffer(Sized, std::size_t count) : count_(count) {
+        if (count == 0) {
+            return;
         }
-        data_ = nullptr;
-        size_ = 0;
+        std::size_t total = 0;
+        if (__builtin_mul_overflow(count, sizeof(T), &total)) {
+            throw std::overflow_error("HostBuffer byte size overflow");
+        }
+        void* pages = nullptr;
+        CUVIT_HIP_CHECK(hipHostMalloc(&pages, total, hipHostMallocDefault));
+        pages_.reset(static_cast<T*>(pages));
     }
 
-    T* data_ = nullptr;
-    std::size_t size_ = 0;
+    std::size_t checked(std::size_t i) const {
+        if (i < count_) {
+            return i;
+        }
+        throw std::out_of_range("HostBuffer index is out of range");
+    }
+
+    std::unique_ptr<T, Unpin> pages_;
+    std::size_t count_ = 0;
 };
 
 template <typename T> void swap(HostBuffer<T>& left, HostBuffer<T>& right) noexcept {

@@ -1,15 +1,20 @@
 #pragma once
 
-// Owning wrapper of a HIP stream, the counterpart of the reference's Stream
-// (include/cuvit/stream.hpp:19-75). Default construction makes a non-blocking
-// stream at the default priority; a moved-from Stream is empty and get()
-// returns nullptr, the default stream.
+// An owned HIP stream. Interface of the reference's Stream
+// (include/cuvit/stream.hpp:19-75): created non-blocking unless flags are
+// given, destroyed with its owner, movable but not copyable; an empty Stream
+// (default-moved-from) hands out nullptr, the null stream.
+//
+// Ownership sits in a unique_ptr whose deleter destroys the stream, so moves,
+// swaps and destruction need no code of their own. Streams keep the default
+// priority.
 
 #include "cuvit/hip_check.hpp"
 
 #include <hip/hip_runtime_api.h>
 
-#include <utility>
+#include <memory>
+#include <type_traits>
 
 namespace cuvit {
 
@@ -17,50 +22,40 @@ class Stream final {
   public:
     Stream() : Stream(hipStreamNonBlocking) {}
 
-    explicit Stream(unsigned int flags) { CUVIT_HIP_CHECK(hipStreamCreateWithFlags(&stream_, flags)); }
+    explicit Stream(unsigned int flags) : handle_(create(flags)) {}
 
-    ~Stream() { release(); }
+    /// Waits for all work queued on the stream.
+    void synchronize() const { CUVIT_HIP_CHECK(hipStreamSynchronize(get())); }
 
-    Stream(const Stream&) = delete;
-    Stream& operator=(const Stream&) = delete;
-
-    Stream(Stream&& other) noexcept : stream_(std::exchange(other.stream_, nullptr)) {}
-
-    Stream& operator=(Stream&& other) noexcept {
-        if (this != &other) {
-            release();
-            stream_ = std::exchange(other.stream_, nullptr);
-        }
-        return *this;
-    }
-
-    /// Blocks until everything queued on the stream has finished.
-    void synchronize() const { CUVIT_HIP_CHECK(hipStreamSynchronize(stream_)); }
-
-    /// True when all queued work has finished; never blocks.
+    /// Whether all queued work has finished, without waiting.
     [[nodiscard]] bool query() const {
-        const hipError_t status = hipStreamQuery(stream_);
-        if (status == hipErrorNotReady) {
-            return false;
+        const hipError_t state = hipStreamQuery(get());
+        if (state != hipErrorNotReady) {
+            CUVIT_HIP_CHECK(state);
         }
-        CUVIT_HIP_CHECK(status);
-        return true;
+        return state == hipSuccess;
     }
 
-    void swap(Stream& other) noexcept { std::swap(stream_, other.stream_); }
+    void swap(Stream& other) noexcept { handle_.swap(other.handle_); }
 
-    [[nodiscard]] hipStream_t get() const noexcept { return stream_; }
-    [[nodiscard]] bool empty() const noexcept { return stream_ == nullptr; }
+    [[nodiscard]] hipStream_t get() const noexcept { return handle_.get(); }
+    [[nodiscard]] bool empty() const noexcept { return !handle_; }
 
   private:
-    void release() noexcept {
-        if (stream_ != nullptr) {
-            static_cast<void>(hipStreamDestroy(stream_));
-            stream_ = nullptr;
+    struct Destroy {
+        void operator()(hipStream_t stream) const noexcept {
+            static_cast<void>(hipStreamDestroy(stream));
         }
+    };
+    using Handle = std::unique_ptr<std::remove_pointer_t<hipStream_t>, Destroy>;
+
+    static Handle create(unsigned int flags) {
+        hipStream_t stream = nullptr;
+        CUVIT_HIP_CHECK(hipStreamCreateWithFlags(&stream, flags));
+        return Handle(stream);
     }
 
-    hipStream_t stream_ = nullptr;
+    Handle handle_;
 };
 
 inline void swap(Stream& left, Stream& right) noexcept { left.swap(right); }
