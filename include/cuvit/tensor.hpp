@@ -1,9 +1,14 @@
 #pragma once
 
-// Non-owning strided view, the counterpart of the reference's TensorView<T>
-// (include/cuvit/tensor.hpp:15-262). Host-only; no HIP include. Strides are in
-// elements. Rank is 1..kMaxTensorRank. Views never own memory: slicing,
-// selecting, transposing and reshaping only change the description.
+// A non-owning, strided view of device or host memory. Interface of the
+// reference's TensorView<T> (include/cuvit/tensor.hpp:15-262): rank 1 to
+// kMaxTensorRank, extents and element strides, offsets of index tuples, and
+// views derived without moving data (slice, select, transpose, reshape).
+// Host-only; nothing here touches the memory it describes.
+//
+// The shape arithmetic lives in Layout, a plain value type; a TensorView is a
+// pointer plus a Layout, and every derived view is a new Layout over an
+// adjusted pointer.
 
 #include <array>
 #include <cstddef>
@@ -21,214 +26,236 @@ inline constexpr int kMaxTensorRank = 4;
 
 using Extent = std::int64_t;
 
+namespace detail {
+
+struct Layout {
+    int rank = 0;
+    std::array<Extent, kMaxTensorRank> extent{};
+    std::array<Extent, kMaxTensorRank> stride{};
+
+    /// A layout of the given extents, strides not yet set.
+    static Layout with_extents(std::initializer_list<Extent> extents) {
+        const std::size_t rank = extents.size();
+        if (rank < 1 || rank > static_cast<std::size_t>(kMaxTensorRank)) {
+            throw std::invalid_argument("A TensorView has rank 1 to " +
+                                        std::to_string(kMaxTensorRank) + ", not " +
+                                        std::to_string(rank));
+        }
+        Layout layout;
+        layout.rank = static_cast<int>(rank);
+        auto out = layout.extent.begin();
+        for (const Extent e : extents) {
+            if (e < 0) {
+                throw std::invalid_argument("TensorView extents cannot be negative");
+            }
+            *out++ = e;
+        }
+        return layout;
+    }
+
+    /// Row-major strides: each axis steps over everything after it.
+    Layout& packed() noexcept {
+        Extent step = 1;
+        for (int a = rank; a-- > 0;) {
+            stride[static_cast<std::size_t>(a)] = step;
+            step *= extent[static_cast<std::size_t>(a)];
+        }
+        return *this;
+    }
+
+    [[nodiscard]] Extent count() const noexcept {
+        Extent total = 1;
+        for (int a = 0; a < rank; ++a) {
+            total *= extent[static_cast<std::size_t>(a)];
+        }
+        return total;
+    }
+
+    /// Row-major dense, where axes of extent one may have any stride.
+    [[nodiscard]] bool dense() const noexcept {
+        Layout reference = *this;
+        reference.packed();
+        for (std::size_t a = 0; a < static_cast<std::size_t>(rank); ++a) {
+            if (extent[a] != 1 && stride[a] != reference.stride[a]) {
+                return false;
+            }
+        }
+        return true;
+    }
+
+    /// @p axis as an array index; out_of_range unless 0 <= axis < rank.
+    [[nodiscard]] std::size_t at(int axis) const {
+        if (axis >= 0 && axis < rank) {
+            return static_cast<std::size_t>(axis);
+        }
+        throw std::out_of_range("Axis " + std::to_string(axis) + " does not exist in a rank-" +
+                                std::to_string(rank) + " TensorView");
+    }
+
+    /// This layout with axis @p a removed.
+    [[nodiscard]] Layout without(std::size_t a) const noexcept {
+        Layout fewer;
+        fewer.rank = rank - 1;
+        for (std::size_t in = 0, out = 0; in < static_cast<std::size_t>(rank); ++in) {
+            if (in == a) {
+                continue;
+            }
+            fewer.extent[out] = extent[in];
+            fewer.stride[out] = stride[in];
+            ++out;
+        }
+        return fewer;
+    }
+};
+
+} // namespace detail
+
 template <typename T> class TensorView {
-    static_assert(!std::is_reference<T>::value, "TensorView cannot view references");
+    static_assert(!std::is_reference<T>::value, "TensorView elements cannot be references");
 
   public:
     using value_type = T;
 
     TensorView() noexcept = default;
 
-    /// Contiguous row-major view of @p data.
-    TensorView(T* data, std::initializer_list<Extent> extents) {
-        set_extents(extents);
-        set_packed_strides();
-        data_ = data;
-        require_data();
-    }
+    /// A dense row-major view of @p data.
+    TensorView(T* data, std::initializer_list<Extent> extents)
+        : TensorView(data, detail::Layout::with_extents(extents).packed()) {}
 
-    /// View with explicit strides.
+    /// A view with the given element strides (non-negative, one per extent).
     static TensorView strided(T* data, std::initializer_list<Extent> extents,
                               std::initializer_list<Extent> strides) {
-        if (extents.size() != strides.size()) {
-            throw std::invalid_argument("TensorView needs one stride per extent");
+        detail::Layout layout = detail::Layout::with_extents(extents);
+        if (strides.size() != extents.size()) {
+            throw std::invalid_argument("A strided TensorView needs as many strides as extents");
         }
-        TensorView view;
-        view.set_extents(extents);
-        int axis = 0;
-        for (const Extent stride : strides) {
-            if (stride < 0) {
+        auto out = layout.stride.begin();
+        for (const Extent s : strides) {
+            if (s < 0) {
                 throw std::invalid_argument("TensorView strides cannot be negative");
             }
-            view.strides_[static_cast<std::size_t>(axis++)] = stride;
+            *out++ = s;
         }
-        view.data_ = data;
-        view.require_data();
-        return view;
+        return TensorView(data, layout);
     }
 
     [[nodiscard]] TensorView<const T> as_const() const noexcept {
-        TensorView<const T> view;
-        view.data_ = data_;
-        view.extents_ = extents_;
-        view.strides_ = strides_;
-        view.rank_ = rank_;
-        return view;
+        return TensorView<const T>(data_, layout_, typename TensorView<const T>::Unchecked{});
     }
 
-    [[nodiscard]] int rank() const noexcept { return rank_; }
-    [[nodiscard]] bool empty() const noexcept { return size() == 0; }
+    [[nodiscard]] int rank() const noexcept { return layout_.rank; }
+    [[nodiscard]] bool empty() const noexcept { return layout_.count() == 0; }
     [[nodiscard]] T* data() const noexcept { return data_; }
-    [[nodiscard]] Extent extent(int axis) const { return extents_[index(axis)]; }
-    [[nodiscard]] Extent stride(int axis) const { return strides_[index(axis)]; }
+    [[nodiscard]] Extent extent(int axis) const { return layout_.extent[layout_.at(axis)]; }
+    [[nodiscard]] Extent stride(int axis) const { return layout_.stride[layout_.at(axis)]; }
 
-    /// Elements addressed by the view (not the size of the allocation).
-    [[nodiscard]] Extent size() const noexcept {
-        Extent total = 1;
-        for (int axis = 0; axis < rank_; ++axis) {
-            total *= extents_[static_cast<std::size_t>(axis)];
-        }
-        return total;
-    }
-
+    /// Elements the view addresses (not the size of the memory behind it).
+    [[nodiscard]] Extent size() const noexcept { return layout_.count(); }
     [[nodiscard]] std::size_t bytes() const noexcept {
-        return static_cast<std::size_t>(size()) * sizeof(T);
+        return static_cast<std::size_t>(layout_.count()) * sizeof(T);
     }
+    [[nodiscard]] bool is_contiguous() const noexcept { return layout_.dense(); }
 
-    /// Dense row-major layout; axes of extent one constrain nothing.
-    [[nodiscard]] bool is_contiguous() const noexcept {
-        Extent expected = 1;
-        for (int axis = rank_ - 1; axis >= 0; --axis) {
-            const auto a = static_cast<std::size_t>(axis);
-            if (extents_[a] == 1) {
-                continue;
-            }
-            if (strides_[a] != expected) {
-                return false;
-            }
-            expected *= extents_[a];
-        }
-        return true;
-    }
-
+    /// The element offset of an index tuple, one index per axis, each in range.
     [[nodiscard]] Extent offset_of(std::initializer_list<Extent> indices) const {
-        if (static_cast<int>(indices.size()) != rank_) {
-            throw std::invalid_argument("TensorView index has the wrong rank");
+        if (static_cast<int>(indices.size()) != layout_.rank) {
+            throw std::invalid_argument("A TensorView of rank " + std::to_string(layout_.rank) +
+                                        " takes " + std::to_string(layout_.rank) + " indices, not " +
+                                        std::to_string(indices.size()));
         }
         Extent offset = 0;
-        std::size_t axis = 0;
+        std::size_t a = 0;
         for (const Extent i : indices) {
-            if (i < 0 || i >= extents_[axis]) {
-                throw std::out_of_range("TensorView index is out of range on axis " +
-                                        std::to_string(axis));
+            if (i < 0 || i >= layout_.extent[a]) {
+                throw std::out_of_range("Index " + std::to_string(i) + " is outside axis " +
+                                        std::to_string(a) + " of extent " +
+                                        std::to_string(layout_.extent[a]));
             }
-            offset += i * strides_[axis];
-            ++axis;
+            offset += i * layout_.stride[a++];
         }
         return offset;
     }
 
-    /// Keeps @p count entries of @p axis starting at @p start; rank unchanged.
+    /// Entries [start, start + count) of @p axis; the rank stays.
     [[nodiscard]] TensorView slice(int axis, Extent start, Extent count) const {
-        const std::size_t a = index(axis);
-        if (start < 0 || count < 0 || start > extents_[a] || count > extents_[a] - start) {
-            throw std::out_of_range("TensorView slice exceeds the extent of axis " +
-                                    std::to_string(axis));
+        const std::size_t a = layout_.at(axis);
+        const Extent length = layout_.extent[a];
+        if (!(start >= 0 && count >= 0 && start <= length && count <= length - start)) {
+            throw std::out_of_range("Slice [" + std::to_string(start) + ", +" +
+                                    std::to_string(count) + ") leaves axis " +
+                                    std::to_string(axis) + " of extent " + std::to_string(length));
         }
-        TensorView view = *this;
-        view.data_ = data_ + start * strides_[a];
-        view.extents_[a] = count;
-        return view;
+        detail::Layout layout = layout_;
+        layout.extent[a] = count;
+        return TensorView(data_ + start * layout_.stride[a], layout, Unchecked{});
     }
 
-    /// Fixes @p axis at @p position and removes it.
+    /// Entry @p position of @p axis, with that axis dropped.
     [[nodiscard]] TensorView select(int axis, Extent position) const {
-        const std::size_t a = index(axis);
-        if (position < 0 || position >= extents_[a]) {
-            throw std::out_of_range("TensorView select is out of range on axis " +
-                                    std::to_string(axis));
+        const std::size_t a = layout_.at(axis);
+        if (position < 0 || position >= layout_.extent[a]) {
+            throw std::out_of_range("Position " + std::to_string(position) + " is outside axis " +
+                                    std::to_string(axis) + " of extent " +
+                                    std::to_string(layout_.extent[a]));
         }
-        TensorView view;
-        view.data_ = data_ + position * strides_[a];
-        view.rank_ = rank_ - 1;
-        std::size_t out = 0;
-        for (std::size_t in = 0; in < static_cast<std::size_t>(rank_); ++in) {
-            if (in != a) {
-                view.extents_[out] = extents_[in];
-                view.strides_[out] = strides_[in];
-                ++out;
-            }
-        }
-        return view;
+        return TensorView(data_ + position * layout_.stride[a], layout_.without(a), Unchecked{});
     }
 
-    /// Swaps two axes; no data moves.
+    /// The view with two axes exchanged; no element moves.
     [[nodiscard]] TensorView transpose(int first, int second) const {
-        const std::size_t a = index(first);
-        const std::size_t b = index(second);
-        TensorView view = *this;
-        std::swap(view.extents_[a], view.extents_[b]);
-        std::swap(view.strides_[a], view.strides_[b]);
-        return view;
+        const std::size_t a = layout_.at(first);
+        const std::size_t b = layout_.at(second);
+        detail::Layout layout = layout_;
+        std::swap(layout.extent[a], layout.extent[b]);
+        std::swap(layout.stride[a], layout.stride[b]);
+        return TensorView(data_, layout, Unchecked{});
     }
 
-    /// New shape over the same elements; only for contiguous views.
+    /// The same elements under new extents; the view must be dense.
     [[nodiscard]] TensorView reshape(std::initializer_list<Extent> extents) const {
-        if (!is_contiguous()) {
-            throw std::invalid_argument("Only a contiguous TensorView can be reshaped");
+        if (!layout_.dense()) {
+            throw std::invalid_argument("A strided TensorView cannot be reshaped");
         }
-        TensorView view;
-        view.set_extents(extents);
-        if (view.size() != size()) {
-            throw std::invalid_argument("TensorView reshape changes the element count");
+        detail::Layout layout = detail::Layout::with_extents(extents);
+        if (layout.count() != layout_.count()) {
+            throw std::invalid_argument("Reshaping " + shape_string() + " to " +
+                                        std::to_string(layout.count()) +
+                                        " elements changes the element count");
         }
-        view.set_packed_strides();
-        view.data_ = data_;
-        return view;
+        return TensorView(data_, layout.packed(), Unchecked{});
     }
 
+    /// "[e0, e1, ...]".
     [[nodiscard]] std::string shape_string() const {
-        std::string text = "[";
-        for (int axis = 0; axis < rank_; ++axis) {
-            text += (axis == 0 ? "" : ", ") + std::to_string(extents_[static_cast<std::size_t>(axis)]);
+        std::string text(1, '[');
+        for (int a = 0; a < layout_.rank; ++a) {
+            if (a != 0) {
+                text += ", ";
+            }
+            text += std::to_string(layout_.extent[static_cast<std::size_t>(a)]);
         }
-        return text + ']';
+        text += ']';
+        return text;
     }
 
   private:
     template <typename U> friend class TensorView;
+    struct Unchecked {};
 
-    void set_extents(std::initializer_list<Extent> extents) {
-        if (extents.size() == 0 || extents.size() > static_cast<std::size_t>(kMaxTensorRank)) {
-            throw std::invalid_argument("TensorView rank must be between 1 and " +
-                                        std::to_string(kMaxTensorRank));
-        }
-        rank_ = static_cast<int>(extents.size());
-        std::size_t axis = 0;
-        for (const Extent e : extents) {
-            if (e < 0) {
-                throw std::invalid_argument("TensorView extents cannot be negative");
-            }
-            extents_[axis++] = e;
+    /// A view of a layout built here or by the caller; a null pointer is only
+    /// allowed when the view is empty.
+    TensorView(T* data, const detail::Layout& layout) : data_(data), layout_(layout) {
+        if (data == nullptr && layout.count() != 0) {
+            throw std::invalid_argument("A TensorView with elements cannot view a null pointer");
         }
     }
 
-    void set_packed_strides() noexcept {
-        Extent stride = 1;
-        for (int axis = rank_ - 1; axis >= 0; --axis) {
-            strides_[static_cast<std::size_t>(axis)] = stride;
-            stride *= extents_[static_cast<std::size_t>(axis)];
-        }
-    }
-
-    void require_data() const {
-        if (data_ == nullptr && size() != 0) {
-            throw std::invalid_argument("A non-empty TensorView cannot view a null pointer");
-        }
-    }
-
-    [[nodiscard]] std::size_t index(int axis) const {
-        if (axis < 0 || axis >= rank_) {
-            throw std::out_of_range("TensorView axis " + std::to_string(axis) +
-                                    " is outside a rank-" + std::to_string(rank_) + " tensor");
-        }
-        return static_cast<std::size_t>(axis);
-    }
+    /// A view derived from a valid one: nothing to check.
+    TensorView(T* data, const detail::Layout& layout, Unchecked) noexcept
+        : data_(data), layout_(layout) {}
 
     T* data_ = nullptr;
-    std::array<Extent, kMaxTensorRank> extents_{};
-    std::array<Extent, kMaxTensorRank> strides_{};
-    int rank_ = 0;
+    detail::Layout layout_{};
 };
 
 } // namespace cuvit

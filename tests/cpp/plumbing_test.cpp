@@ -27,6 +27,7 @@
 #include <fstream>
 #include <functional>
 #include <iostream>
+#include <iterator>
 #include <stdexcept>
 #include <string>
 #include <type_traits>
@@ -292,6 +293,14 @@ void device_buffer_copies_and_bounds() {
     buffer.copy_from_device(buffer, 10, 0, 500);
     buffer.copy_to_host(part.data(), 10, 500);
     require(part[0] == 0.0F && part[9] == 9.0F, "disjoint self copy");
+    buffer.copy_from_device(buffer, 10, 500, 510);  // adjacent ranges touch but do not overlap
+    buffer.copy_from_device(buffer, 10, 520, 510);
+    require_throws<std::invalid_argument>([&] { buffer.copy_from_device(buffer, 10, 519, 510); },
+                                          "self copy overlapping by one element");
+    require_throws<std::out_of_range>([&] { buffer.copy_from_device(buffer, 1, 1000, 0); },
+                                      "source offset at the end");
+    buffer.copy_from_device(buffer, 0, 1000, 1000);  // empty copies at the end are fine
+    buffer.copy_to_host(nullptr, 0, 1000);
 
     cuvit::DeviceBuffer<float> moved(std::move(buffer));
     require(buffer.empty() && buffer.data() == nullptr && buffer.device() == -1, "moved-from");
@@ -306,6 +315,11 @@ void device_buffer_copies_and_bounds() {
     require(moved.data() == before, "same size keeps the allocation");
     moved.reset();
     require(moved.empty(), "reset");
+    require(moved.data() == nullptr && moved.device() == -1, "reset releases the allocation");
+    moved.allocate(3);
+    require(moved.size() == 3 && moved.device() == device, "allocate after reset");
+    moved.allocate(0);
+    require(moved.empty() && moved.data() == nullptr, "allocate(0) releases");
 }
 
 // -- device: HostBuffer (reference host_buffer_test.cu) -----------------------
@@ -325,6 +339,14 @@ void host_buffer_is_pinned_and_usable() {
     require(pinned.data() == before && pinned[7] == 14.0F, "same size keeps contents");
     cuvit::HostBuffer<float> moved(std::move(pinned));
     require(pinned.empty() && moved.size() == 4096, "move");
+    cuvit::HostBuffer<float> other(8);
+    other = std::move(moved);
+    require(moved.empty() && moved.data() == nullptr && other.size() == 4096 && other[7] == 14.0F,
+            "move assignment");
+    moved = std::move(other);
+    require(std::distance(moved.begin(), moved.end()) == 4096, "iteration covers the elements");
+    other.allocate(0);
+    require(other.empty() && other.data() == nullptr, "allocate(0) keeps nothing");
 
     cuvit::DeviceBuffer<float> device(moved.size());
     cuvit::Stream stream;
