@@ -12,6 +12,7 @@
 // Both tiles of a type run the same MFMA over K in the same order, so the
 // choice never changes a result.
 #include "gemm_kernel.hpp"
+#include "gemm_wide.hpp"
 
 namespace cuvit::detail {
 namespace {
@@ -147,8 +148,65 @@ hipError_t gemm_f32(const float* a, const float* b, const float* bias, float* c,
     return pick_flags<float, 2, 2, 1, 1, 32>(a, b, bias, c, args, stream);
 }
 
+/// The wide-tile kernel (gemm_wide.hpp) for a problem it covers: B as [N, K],
+/// A and B vector operands within one descriptor's span, C written whole in
+/// 16-byte pieces (N, ldc and the C strides multiples of 8, C 16-byte aligned),
+/// no accumulation and no addend, and enough 128 x 256 tiles to fill every
+/// CU's two slots. Returns hipErrorNotSupported otherwise.
+template <int TM, int TN>
+hipError_t launch_wide(const std::uint16_t* a, const std::uint16_t* b, const float* bias,
+                       std::uint16_t* c, const GemmArgs& args, hipStream_t stream) {
+    using S = gemm::WideShape<TM, TN>;
+    const bool split = args.inner > 0;
+    const bool eligible =
+        args.transposed && !args.accumulate && args.addend == nullptr &&
+        vector_operand(a, args.lda, args.k, args.stride_a, args.outer_stride_a, split) &&
+        vector_operand(b, args.ldb, args.k, args.stride_b, args.outer_stride_b, split) &&
+        static_cast<std::int64_t>(S::kBM) * args.lda * 2 < gemm::kMaxSpan &&
+        static_cast<std::int64_t>(S::kBN) * args.ldb * 2 < gemm::kMaxSpan && aligned16(c) &&
+        args.n % 8 == 0 && args.ldc % 8 == 0 && args.stride_c % 8 == 0 &&
+        (!split || args.outer_stride_c % 8 == 0) &&
+        tile_count(args, S::kBM, S::kBN) >= static_cast<std::int64_t>(compute_units()) * 2;
+    if (!eligible) {
+        return hipErrorNotSupported;
+    }
+    const gemm::TileMap map = tile_map(args, S::kBM, S::kBN, 2);
+    const std::int64_t tiles_m = (args.m + S::kBM - 1) / S::kBM;
+    const std::int64_t tiles_n = (args.n + S::kBN - 1) / S::kBN;
+    const std::int64_t tiles = map.px > 0 ? 8 * ((tiles_m + map.px - 1) / map.px) *
+                                                ((tiles_n + map.py - 1) / map.py)
+                                          : tiles_m * tiles_n;
+    if (tiles > 0x7FFFFFFF) {
+        return hipErrorNotSupported;
+    }
+    const dim3 grid(static_cast<unsigned int>(tiles),
+                    static_cast<unsigned int>(args.count < kMaxGridY ? args.count : kMaxGridY));
+    auto run = [&](auto kernel) -> hipError_t {
+        static std::atomic<std::uint64_t> opted_in{0};
+        if (const hipError_t opted =
+                allow_lds(reinterpret_cast<const void*>(kernel), S::kLdsBytes, opted_in);
+            opted != hipSuccess) {
+            return opted;
+        }
+        kernel<<<grid, kThreads, S::kLdsBytes, stream>>>(a, b, bias, c, args, map);
+        return hipGetLastError();
+    };
+    if (bias != nullptr) {
+        return args.gelu ? run(gemm::gemm_wide_kernel<TM, TN, true, true>)
+                         : run(gemm::gemm_wide_kernel<TM, TN, true, false>);
+    }
+    return args.gelu ? run(gemm::gemm_wide_kernel<TM, TN, false, true>)
+                     : run(gemm::gemm_wide_kernel<TM, TN, false, false>);
+}
+
 hipError_t gemm_bf16(const std::uint16_t* a, const std::uint16_t* b, const float* bias,
                      std::uint16_t* c, const GemmArgs& args, hipStream_t stream) {
+    // 128 x 256 tiles with 64 x 128 per wavefront (ViT-Base FC1 + GELU 137 ->
+    // 110 us), where they apply; bitwise the same results as the tiles below.
+    if (const hipError_t wide = launch_wide<2, 4>(a, b, bias, c, args, stream);
+        wide != hipErrorNotSupported) {
+        return wide;
+    }
     if (tile_count(args, 128, 128) >= static_cast<std::int64_t>(compute_units()) * 2) {
         // Up to K = 1024, 32-deep stages with registers for three workgroups
         // per CU beat 64-deep ones at two (ViT-Base FC1 + GELU 146 -> 136 us,

@@ -113,6 +113,9 @@ __device__ __forceinline__ Offsets entry_offsets(const GemmArgs& args, int entry
 /// the store.
 __device__ __forceinline__ float epilogue_value(float sum, const float* bias, int row, int column,
                                                 const GemmArgs& args) {
+    // alpha * sum and each addition round on their own (no fused multiply-add),
+    // the reference's order, in every GEMM kernel alike.
+#pragma clang fp contract(off)
     float value = args.alpha * sum;
     if (bias != nullptr) {
         value += bias[column];
