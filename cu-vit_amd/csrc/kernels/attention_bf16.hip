@@ -75,6 +75,8 @@ constexpr int kWavesPerGroup = 4;
 
 /// Elements per LDS row of K ([key][head_dim + 8]).
 constexpr int kKeyPitch = kHeadDim + 8;
+/// 16-byte chunks of one key's K or V row.
+constexpr int kChunksPerKey = kHeadDim / 8;
 
 /// V ([key][head_dim]), then K.
 __host__ __device__ constexpr std::size_t lds_bytes(int key_tiles) {
@@ -126,52 +128,118 @@ __device__ __forceinline__ std::uint32_t exchange(std::uint32_t value) {
 }
 
 __device__ __forceinline__ std::uint32_t pack_bf16(float low, float high) {
-    return static_cast<std::uint32_t>(float_to_bf16(low)) |
-           (static_cast<std::uint32_t>(float_to_bf16(high)) << 16);
+    return pack_bf16x2(low, high);
+}
+
+/// The (image, head) pair's query, key and value bases in the packed
+/// [images, tokens, 3, heads, 64] projection.
+struct PairBases {
+    const std::uint16_t* q;
+    const std::uint16_t* k;
+    const std::uint16_t* v;
+    int image;
+    int head;
+};
+
+__device__ __forceinline__ PairBases pair_bases(const std::uint16_t* qkv, int pair, int heads,
+                                                int tokens) {
+    const int image = pair / heads;
+    const int head = pair - image * heads;
+    const std::int64_t qkv_row = 3 * static_cast<std::int64_t>(heads) * kHeadDim;
+    const std::uint16_t* const q =
+        qkv + static_cast<std::int64_t>(image) * tokens * qkv_row + head * kHeadDim;
+    return {q, q + heads * kHeadDim, q + 2 * heads * kHeadDim, image, head};
 }
 
 /// @tparam KT 32-key tiles covering the tokens.
-template <int KT>
+/// @tparam Chunks per thread of a pair's K and V (ceil(2 * KT * 32 * 8 / threads)) when the
+///   workgroup loops over several pairs and prefetches the next pair's K and V into
+///   registers while it works on the current one; 0 for one pair per workgroup.
+template <int KT, int Chunks>
 __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
     const std::uint16_t* __restrict__ qkv, std::uint16_t* __restrict__ context, int heads,
-    int tokens, float scale) {
+    int tokens, int pairs, float scale) {
     constexpr int kPadded = KT * kEdge;
+    constexpr int kBufferElements = kPadded * (kHeadDim + kKeyPitch);
     extern __shared__ Vec16 lds_vectors[];
-    std::uint16_t* const values = reinterpret_cast<std::uint16_t*>(lds_vectors); // [kPadded][64]
-    std::uint16_t* const keys = values + kPadded * kHeadDim;                     // [kPadded][72]
+    std::uint16_t* const lds = reinterpret_cast<std::uint16_t*>(lds_vectors);
     const int waves = static_cast<int>(blockDim.x) / kWave;
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     const int lane = lane_id();
     const int row = lane % kEdge;  // fragment row: query (logits) or dim (V)
     const int half = lane / kEdge; // which half of a run pair the lane holds
     const int chunk = 8 * half;    // fragment k offset
-
-    const int pair = blockIdx.y;
-    const int image = pair / heads;
-    const int head = pair - image * heads;
     const int embed = heads * kHeadDim;
     const std::int64_t qkv_row = 3 * static_cast<std::int64_t>(embed);
-    const std::uint16_t* const q_base =
-        qkv + static_cast<std::int64_t>(image) * tokens * qkv_row + head * kHeadDim;
-    const std::uint16_t* const k_base = q_base + embed;
-    const std::uint16_t* const v_base = q_base + 2 * embed;
-
-    // V and K into LDS, shared by the workgroup's query tiles; keys past the
-    // tokens are zero.
     constexpr int kChunks = kHeadDim / 8;
-    for (int c = threadIdx.x; c < kPadded * kChunks; c += blockDim.x) {
-        const int key = c / kChunks;
-        const int d0 = 8 * (c % kChunks);
-        const Vec16 v = load_or_zero(v_base, key * qkv_row + d0, key < tokens);
-        const Vec16 k = load_or_zero(k_base, key * qkv_row + d0, key < tokens);
-        store16(values + value_slot(key, d0), v);
-        store16(keys + key * kKeyPitch + d0, k);
-    }
+
+    // V and K of a pair into LDS buffer `buffer` ([kPadded][64] V, then
+    // [kPadded][72] K), straight from global memory; keys past the tokens are zero.
+    auto load_direct = [&](const PairBases& b, int buffer) {
+        std::uint16_t* const values = lds + buffer * kBufferElements;
+        std::uint16_t* const keys = values + kPadded * kHeadDim;
+        for (int c = threadIdx.x; c < kPadded * kChunks; c += blockDim.x) {
+            const int key = c / kChunks;
+            const int d0 = 8 * (c % kChunks);
+            const Vec16 v = load_or_zero(b.v, key * qkv_row + d0, key < tokens);
+            const Vec16 k = load_or_zero(b.k, key * qkv_row + d0, key < tokens);
+            store16(values + value_slot(key, d0), v);
+            store16(keys + key * kKeyPitch + d0, k);
+        }
+    };
+    // The same through registers: chunk c of the pair's 2 * kPadded * 8 is
+    // thread (c % threads)'s element c / threads; V's chunks first.
+    Vec16 ahead[Chunks > 0 ? Chunks : 1];
+    auto prefetch = [&](const PairBases& b) {
+#pragma unroll
+        for (int i = 0; i < Chunks; ++i) {
+            const int c = static_cast<int>(threadIdx.x) + i * static_cast<int>(blockDim.x);
+            const bool is_key = c >= kPadded * kChunks;
+            const int cc = is_key ? c - kPadded * kChunks : c;
+            const int key = cc / kChunks;
+            const int d0 = 8 * (cc % kChunks);
+            ahead[i] = load_or_zero(is_key ? b.k : b.v, key * qkv_row + d0,
+                                    c < 2 * kPadded * kChunks && key < tokens);
+        }
+    };
+    auto commit = [&](int buffer) {
+        std::uint16_t* const values = lds + buffer * kBufferElements;
+        std::uint16_t* const keys = values + kPadded * kHeadDim;
+#pragma unroll
+        for (int i = 0; i < Chunks; ++i) {
+            const int c = static_cast<int>(threadIdx.x) + i * static_cast<int>(blockDim.x);
+            if (c < 2 * kPadded * kChunks) {
+                const bool is_key = c >= kPadded * kChunks;
+                const int cc = is_key ? c - kPadded * kChunks : c;
+                const int key = cc / kChunks;
+                const int d0 = 8 * (cc % kChunks);
+                if (is_key) {
+                    store16(keys + key * kKeyPitch + d0, ahead[i]);
+                } else {
+                    store16(values + value_slot(key, d0), ahead[i]);
+                }
+            }
+        }
+    };
+
+    int pair = static_cast<int>(blockIdx.y);
+    int buffer = 0;
+    load_direct(pair_bases(qkv, pair, heads, tokens), 0);
     __syncthreads();
-    const int query0 = (static_cast<int>(blockIdx.x) * waves + wave) * kEdge;
-    if (query0 >= tokens) {
-        return; // no barrier follows
+    for (;;) {
+    const int next = pair + static_cast<int>(gridDim.y);
+    const bool more = Chunks > 0 && next < pairs;
+    if (more) {
+        prefetch(pair_bases(qkv, next, heads, tokens));
     }
+    const PairBases bases = pair_bases(qkv, pair, heads, tokens);
+    const std::uint16_t* const q_base = bases.q;
+    const int image = bases.image;
+    const int head = bases.head;
+    const std::uint16_t* const values = lds + buffer * kBufferElements;
+    const std::uint16_t* const keys = values + kPadded * kHeadDim;
+    const int query0 = (static_cast<int>(blockIdx.x) * waves + wave) * kEdge;
+    if (query0 < tokens) {
     const int query = query0 + row;
 
     // Logits tiles: the GEMM's MFMA and operand roles, alpha * sum rounded
@@ -204,7 +272,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
         for (int i = 0; i < 16; ++i) {
             const int key = kt * kEdge + Bf16Mma::column(lane, i / 4) + i % 4;
             x[kt][i] = bf16_to_float(float_to_bf16(scale * x[kt][i]));
-            if (key < tokens) {
+            // Only the last key tile holds keys past the tokens.
+            if (kt < KT - 1 || key < tokens) {
                 maximum = fmaxf(maximum, x[kt][i]);
             }
         }
@@ -217,7 +286,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int key = kt * kEdge + Bf16Mma::column(lane, i / 4) + i % 4;
-            x[kt][i] = key < tokens ? shifted_exp(x[kt][i], maximum) : 0.F;
+            x[kt][i] = kt < KT - 1 || key < tokens ? shifted_exp(x[kt][i], maximum) : 0.F;
         }
     }
 
@@ -279,23 +348,31 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
     // weights.V over the GEMM's k-blocks: its 64-key stages run in pairs.
     constexpr int kStages = (kPadded + kStage - 1) / kStage;
     constexpr int kBlocks = (kStages + 1) / 2 * 2 * (kStage / kKBlock);
+    // The two 32-dim halves accumulate side by side (two independent MFMA
+    // chains); each keeps the k-block order above.
+    Acc acc2[2];
 #pragma unroll
-    for (int d0 = 0; d0 < kHeadDim; d0 += kEdge) {
-        Acc acc;
+    for (int d = 0; d < 2; ++d)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            acc[i] = 0.F;
+            acc2[d][i] = 0.F;
         }
 #pragma unroll
-        for (int kb = 0; kb < kBlocks; ++kb) {
+    for (int kb = 0; kb < kBlocks; ++kb) {
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
             if (kb < 2 * KT) {
-                const Vec16 v = value_fragment(values, kb, d0, lane);
-                Bf16Mma::run(acc, v, fragment[kb]);
+                const Vec16 v = value_fragment(values, kb, d * kEdge, lane);
+                Bf16Mma::run(acc2[d], v, fragment[kb]);
             } else {
                 const Vec16 zero{{0U, 0U, 0U, 0U}};
-                Bf16Mma::run(acc, zero, zero);
+                Bf16Mma::run(acc2[d], zero, zero);
             }
         }
+    }
+#pragma unroll
+    for (int d0 = 0; d0 < kHeadDim; d0 += kEdge) {
+        const Acc& acc = acc2[d0 / kEdge];
         if (query < tokens) {
             std::uint16_t* const out = context +
                                        (static_cast<std::int64_t>(image) * tokens + query) * embed +
@@ -309,6 +386,16 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
             }
         }
     }
+    }  // query0 < tokens
+    if (!more) {
+        break;
+    }
+    commit(buffer ^ 1);
+    // Every wavefront is done with this pair's buffer and the next one's is whole.
+    __syncthreads();
+    buffer ^= 1;
+    pair = next;
+    }
 }
 
 template <int KT>
@@ -320,21 +407,44 @@ hipError_t launch(const std::uint16_t* qkv, std::uint16_t* context, int images, 
     // four below that (ViT-Tiny b32: 11.4 us against 14.8 with seven).
     const int query_tiles = (tokens + kEdge - 1) / kEdge;
     const std::int64_t pairs = static_cast<std::int64_t>(images) * heads;
-    const int per_group = pairs >= 2 * static_cast<std::int64_t>(compute_units()) ? kMaxWaves
-                                                                                  : kWavesPerGroup;
+    const bool many = pairs >= 2 * static_cast<std::int64_t>(compute_units());
+    const int per_group = many ? kMaxWaves : kWavesPerGroup;
     const int waves = query_tiles < per_group ? query_tiles : per_group;
+    const float scale = 1.0F / std::sqrt(static_cast<float>(kHeadDim));
+    // (Up to 7 key tiles, 224 tokens: with 8 the prefetch registers spill.)
+    if constexpr (KT <= 7) {
+    if (many && pairs <= 0x7FFFFFFF) {
+        // One workgroup per CU (the kernel's registers allow one of KT
+        // wavefronts) looping over pairs, the next pair's K and V loaded into
+        // registers during the current pair's work and into the second LDS
+        // buffer after it: each CU's later pairs do not wait for their loads.
+        // With waves = KT, a thread's share of a pair's K and V is 8 chunks.
+        constexpr int kChunksPerThread = 2 * kEdge * kChunksPerKey / kWave;
+        auto kernel = attention_bf16_kernel<KT, kChunksPerThread>;
+        static std::atomic<std::uint64_t> opted_in{0};
+        if (const hipError_t opted =
+                allow_lds(reinterpret_cast<const void*>(kernel), 2 * lds_bytes(KT), opted_in);
+            opted != hipSuccess) {
+            return opted;
+        }
+        const std::int64_t groups = compute_units() < pairs ? compute_units() : pairs;
+        kernel<<<dim3(1, static_cast<unsigned int>(groups)), query_tiles * kWave, 2 * lds_bytes(KT),
+                 stream>>>(qkv, context, heads, tokens, static_cast<int>(pairs), scale);
+        return hipGetLastError();
+    }
+    }
     // Above 64 KiB (256 tokens) the kernel opts in to more LDS, once per device.
+    auto kernel = attention_bf16_kernel<KT, 0>;
     static std::atomic<std::uint64_t> opted_in{0};
-    if (const hipError_t opted = allow_lds(reinterpret_cast<const void*>(attention_bf16_kernel<KT>),
-                                           lds_bytes(KT), opted_in);
+    if (const hipError_t opted = allow_lds(reinterpret_cast<const void*>(kernel), lds_bytes(KT),
+                                           opted_in);
         opted != hipSuccess) {
         return opted;
     }
     const dim3 grid(static_cast<unsigned int>((query_tiles + waves - 1) / waves),
                     static_cast<unsigned int>(pairs));
-    const float scale = 1.0F / std::sqrt(static_cast<float>(kHeadDim));
-    attention_bf16_kernel<KT><<<grid, waves * kWave, lds_bytes(KT), stream>>>(qkv, context, heads,
-                                                                               tokens, scale);
+    kernel<<<grid, waves * kWave, lds_bytes(KT), stream>>>(qkv, context, heads, tokens,
+                                                          static_cast<int>(pairs), scale);
     return hipGetLastError();
 }
 

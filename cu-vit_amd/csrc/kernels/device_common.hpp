@@ -75,6 +75,16 @@ __device__ __forceinline__ std::uint16_t float_to_bf16(float value) {
     return __builtin_bit_cast(std::uint16_t, static_cast<__bf16>(value));
 }
 
+/// Two floats rounded to bf16 and packed (@p low in bits 0-15), by one
+/// v_cvt_pk_bf16_f32: the same rounding as float_to_bf16 on each, in one
+/// instruction instead of two conversions, a shift and an or.
+__device__ __forceinline__ std::uint32_t pack_bf16x2(float low, float high) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float floatx2 __attribute__((ext_vector_type(2)));
+    const floatx2 pair = {low, high};
+    return __builtin_bit_cast(std::uint32_t, __builtin_convertvector(pair, bf16x2));
+}
+
 // -- erf GELU -------------------------------------------------------------------
 
 /// GELU in its erf form, x * Phi(x) = 0.5 x (1 + erf(x / sqrt 2)), branch-free.

@@ -233,10 +233,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_wide_kernel(const std::uint1
                         v[e] = kGelu ? gelu(x) : x;
                     }
                     uint2 bits;
-                    bits.x = static_cast<std::uint32_t>(float_to_bf16(v[0])) |
-                             (static_cast<std::uint32_t>(float_to_bf16(v[1])) << 16);
-                    bits.y = static_cast<std::uint32_t>(float_to_bf16(v[2])) |
-                             (static_cast<std::uint32_t>(float_to_bf16(v[3])) << 16);
+                    bits.x = pack_bf16x2(v[0], v[1]);
+                    bits.y = pack_bf16x2(v[2], v[3]);
                     const int chunk = (wave_n * TN * E + j * E) / 8 + q;
                     *reinterpret_cast<uint2*>(tile + r * (BN * 2) +
                                               ((chunk ^ (r % kTileChunks)) * 16) + (lane / 32) * 8) =
