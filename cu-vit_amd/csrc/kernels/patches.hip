@@ -126,9 +126,17 @@ __global__ __launch_bounds__(kBlock) void extract_patches_strip_kernel(
 /// batch 32 this took the gather from 8.87 us (strip kernel) to 7.52 us on one
 /// MI355X, where a same-bytes copy took 7.72 us. The same loads and stores
 /// issued in one batch (all loads, then all stores) took 8.25-8.60 us.
+///
+/// @tparam kHeight, kWidth the image geometry when known at compile time (224 x 224,
+///   ViT/16's), 0 for the runtime arguments: with constants the task's index
+///   math becomes shifts and multiplies by constants instead of divisions and
+///   32-bit multiplies by runtime values, all of it ahead of the first loads.
+template <int kHeight, int kWidth>
 __global__ __launch_bounds__(kWave) void extract_patches_pair_kernel(
-    const unsigned char* __restrict__ images, unsigned char* __restrict__ patches, int height,
-    int width, int tasks) {
+    const unsigned char* __restrict__ images, unsigned char* __restrict__ patches,
+    int height_argument, int width_argument, int tasks) {
+    const int height = kHeight > 0 ? kHeight : height_argument;
+    const int width = kWidth > 0 ? kWidth : width_argument;
     constexpr int kChannels = 3;
     constexpr int kPatch = 16;
     constexpr int kElement = 4;
@@ -336,9 +344,11 @@ hipError_t dispatch_patches(const void* images, void* patches, int batch, int ch
         // Task indices, and a task plus the grid, stay below 2^31.
         if (tasks <= 0x3fffffff) {
             const std::int64_t grid = (tasks + 1) / 2;  // two tasks per wavefront
-            extract_patches_pair_kernel<<<static_cast<unsigned int>(grid), kWave, 0, stream>>>(
-                    static_cast<const unsigned char*>(images), static_cast<unsigned char*>(patches),
-                    height, width, static_cast<int>(tasks));
+            auto kernel = height == 224 && width == 224 ? extract_patches_pair_kernel<224, 224>
+                                                        : extract_patches_pair_kernel<0, 0>;
+            kernel<<<static_cast<unsigned int>(grid), kWave, 0, stream>>>(
+                static_cast<const unsigned char*>(images), static_cast<unsigned char*>(patches),
+                height, width, static_cast<int>(tasks));
             return hipGetLastError();
         }
     }
