@@ -91,31 +91,36 @@ __device__ __forceinline__ std::uint32_t pack_bf16x2(float low, float high) {
 /// With z = |x| / sqrt 2 and t = 1 / (1 + z / 2),
 ///   erfc(z) = t exp(-z^2 + P(t)),
 /// the functional form of the Chebyshev erfc of Press et al., Numerical
-/// Recipes 6.2; P is this library's own degree-9 fit (gelu_fit.py in this
+/// Recipes 6.2; P is this library's own degree-7 fit (gelu_fit.py in this
 /// folder: Chebyshev interpolation in float64 over z in [0, 10], largest error
-/// of P 4.8e-8, which is erfc's relative error). Then Phi(x) = erfc(z) / 2 for
-/// x < 0 and 1 - erfc(z) / 2 otherwise, so the negative tail keeps its
-/// relative accuracy instead of cancelling in 1 + erf. Emulated in float32
-/// over [-12, 12] against float64: at most 3.8e-7 absolute error (a
-/// correctly rounded erf in the textbook formula: 4.5e-7), inside the
-/// reference's GELU tolerance (rtol 1e-5, atol 1e-6; elementwise_test.cu:48-49).
-/// About 20 instructions, against ~40 with two divergent branches for erff.
+/// of P 7.4e-7, which is erfc's relative error). The evaluation runs in base 2
+/// with every constant folded in: w = z sqrt(log2 e), so -z^2 log2 e = -w^2
+/// and 1 + z / 2 = 1 + w / (2 sqrt(log2 e)), and Q = P log2 e - 1 also
+/// carries the factor 1/2, so that
+///   erfc(z) / 2 = t exp2(-w^2 + Q(t))
+/// takes one fused multiply-add and one exp2. Then Phi(x) = erfc(z) / 2 for
+/// x < 0 and 1 - erfc(z) / 2 (one fused multiply-add) otherwise, so the
+/// negative tail keeps its relative accuracy instead of cancelling in 1 + erf. Emulated in float32
+/// over [-12, 12] against float64: at most 3.8e-7 absolute error, 5.4e-6
+/// relative over the tail [-9, -3], inside the reference's GELU tolerance
+/// (rtol 1e-5, atol 1e-6; elementwise_test.cu:48-49); rounded to bf16, about
+/// 5e-5 of normally distributed inputs land one ulp from the correctly
+/// rounded GELU. 17 instructions, two of them transcendental (rcp, exp2):
+/// the GELU of a GEMM epilogue costs about as much issue time as the MFMAs
+/// of a K = 768 product, so every instruction counts here.
 __device__ __forceinline__ float gelu(float x) {
-    const float z = fabsf(x) * 0.70710678118654752F;
-    const float t = __builtin_amdgcn_rcpf(fmaf(0.5F, z, 1.0F));
-    float p = 1.449302143e-01F;
-    p = fmaf(p, t, -6.808271813e-01F);
-    p = fmaf(p, t, 1.156733766e+00F);
-    p = fmaf(p, t, -6.962519109e-01F);
-    p = fmaf(p, t, -8.028042193e-02F);
-    p = fmaf(p, t, 1.267580721e-03F);
-    p = fmaf(p, t, 3.460280200e-02F);
-    p = fmaf(p, t, 3.866404117e-01F);
-    p = fmaf(p, t, 9.986327834e-01F);
-    p = fmaf(p, t, -1.265447997e+00F);
-    const float erfc_z = t * __builtin_amdgcn_exp2f(fmaf(-z, z, p) * 1.4426950408889634F);
-    const float half = 0.5F * erfc_z;
-    return x * (x < 0.0F ? half : 1.0F - half);
+    const float w = fabsf(x) * 0.84932180028801907F;                              // sqrt(log2(e) / 2)
+    const float t = __builtin_amdgcn_rcpf(fmaf(w, 0.41627730557884884F, 1.0F));  // 1 / (2 sqrt(log2 e))
+    float q = -2.718776930e-01F;
+    q = fmaf(q, t, 1.087971315e+00F);
+    q = fmaf(q, t, -1.449840281e+00F);
+    q = fmaf(q, t, 5.090884594e-01F);
+    q = fmaf(q, t, -5.895698485e-02F);
+    q = fmaf(q, t, 5.686708691e-01F);
+    q = fmaf(q, t, 1.440642000e+00F);
+    q = fmaf(q, t, -2.825698747e+00F);
+    const float e = __builtin_amdgcn_exp2f(fmaf(-w, w, q));  // erfc(z) / 2 = t e
+    return x * (x < 0.0F ? t * e : fmaf(-t, e, 1.0F));
 }
 
 // -- 16-byte vectors ----------------------------------------------------------

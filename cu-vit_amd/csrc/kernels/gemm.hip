@@ -191,12 +191,16 @@ hipError_t launch_wide(const std::uint16_t* a, const std::uint16_t* b, const flo
         kernel<<<grid, kThreads, S::kLdsBytes, stream>>>(a, b, bias, c, args, map);
         return hipGetLastError();
     };
-    if (bias != nullptr) {
-        return args.gelu ? run(gemm::gemm_wide_kernel<TM, TN, true, true>)
-                         : run(gemm::gemm_wide_kernel<TM, TN, true, false>);
-    }
-    return args.gelu ? run(gemm::gemm_wide_kernel<TM, TN, false, true>)
-                     : run(gemm::gemm_wide_kernel<TM, TN, false, false>);
+    auto pick = [&](auto with_alpha) -> hipError_t {
+        constexpr bool kAlpha = decltype(with_alpha)::value;
+        if (bias != nullptr) {
+            return args.gelu ? run(gemm::gemm_wide_kernel<TM, TN, true, true, kAlpha>)
+                             : run(gemm::gemm_wide_kernel<TM, TN, true, false, kAlpha>);
+        }
+        return args.gelu ? run(gemm::gemm_wide_kernel<TM, TN, false, true, kAlpha>)
+                         : run(gemm::gemm_wide_kernel<TM, TN, false, false, kAlpha>);
+    };
+    return args.alpha == 1.0F ? pick(std::false_type{}) : pick(std::true_type{});
 }
 
 hipError_t gemm_bf16(const std::uint16_t* a, const std::uint16_t* b, const float* bias,

@@ -20,8 +20,8 @@
 // and which one runs depends on the shape only.
 //
 // Epilogue. alpha, the bias and GELU are applied in registers (the bias for
-// the lane's 64 columns loaded after the k loop, the flags as template
-// parameters), each
+// the lane's 64 columns loaded after the k loop; the flags, and whether alpha
+// differs from 1, as template parameters: 1 * x is x, bit for bit), each
 // value rounded once to bf16 and written into the LDS as a [BM][BN] tile with
 // 16-byte chunk c of row r at c ^ (r % chunks_per_row); after a barrier each
 // wavefront reads whole rows back and stores them with 16-byte non-temporal
@@ -60,7 +60,7 @@ template <int TM, int TN> struct WideShape {
     }
 };
 
-template <int TM, int TN, bool kBias, bool kGelu>
+template <int TM, int TN, bool kBias, bool kGelu, bool kAlpha>
 __global__ __launch_bounds__(kThreads, 2) void gemm_wide_kernel(const std::uint16_t* __restrict__ a,
                                                                const std::uint16_t* __restrict__ b,
                                                                const float* __restrict__ bias,
@@ -197,20 +197,27 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_wide_kernel(const std::uint1
         }
 
         // Epilogue through LDS: the k loop ended on a barrier, so the stage
-        // buffers are free. The bias of the lane's 64 columns (tile j, run q,
-        // element e) is loaded here, all loads in flight together (held over
-        // the k loop it would cost the registers of a second workgroup).
+        // buffers are free. The bias of the lane's 64 columns (tile j, run q
+        // of four columns) comes in 16 buffer loads of 16 bytes, all in
+        // flight together, columns past N reading as zero (held over the k
+        // loop it would cost the registers of a second workgroup).
         float column_bias[TN][4][4];
+        if constexpr (kBias) {
+            const auto bias_resource = buffer_resource(bias);
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+            for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int col = col0 + wave_n * TN * E + j * E + Mma<std::uint16_t>::column(lane, q);
+                for (int q = 0; q < 4; ++q) {
+                    const int col = col0 + wave_n * TN * E + j * E + Mma<std::uint16_t>::column(lane, q);
+                    // N is a multiple of 8 here, so a run of four starts and ends inside
+                    const Vec16 v = buffer_load16(
+                        bias_resource, col < args.n ? static_cast<unsigned int>(col) * 4U : kOutside);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    column_bias[j][q][e] = kBias && col + e < args.n ? bias[col + e] : 0.F;
+                    for (int e = 0; e < 4; ++e) {
+                        column_bias[j][q][e] = __uint_as_float(v.w[e]);
+                    }
                 }
-            }
+        }
         constexpr int kTileChunks = BN / 8;  // 16-byte chunks per row of the C tile
         unsigned char* const tile = reinterpret_cast<unsigned char*>(lds);
 #pragma unroll
@@ -226,7 +233,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_wide_kernel(const std::uint1
                         // The order of gemm_kernel.hpp's epilogue_value: alpha * sum,
                         // then the bias, each rounded on its own.
 #pragma clang fp contract(off)
-                        float x = args.alpha * acc[i][j][4 * q + e];
+                        float x = kAlpha ? args.alpha * acc[i][j][4 * q + e] : acc[i][j][4 * q + e];
                         if constexpr (kBias) {
                             x += column_bias[j][q][e];
                         }
