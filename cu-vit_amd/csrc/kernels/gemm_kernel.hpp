@@ -19,10 +19,11 @@
 // each stage costs one barrier.
 //
 // MFMA. fp32 uses v_mfma_f32_16x16x4_f32 (E = 16) and bf16
-// v_mfma_f32_32x32x16_bf16 (E = 32); measured on MI355X these issue at
-// 127 TFLOP/s and 2.1 PFLOP/s, while bf16's 16 x 16 form reaches only
-// 1.2 PFLOP/s, and fp32's fine 16 x 16 tiles fit ViT-Tiny's 192- and
-// 197-wide shapes. Lane l reads one 16-byte fragment per operand per k-block:
+// v_mfma_f32_32x32x16_bf16 (E = 32); measured on MI355X with an in-kernel
+// cycle counter, the fp32 one issues every 32 core cycles even as a single
+// dependent chain (the full rate; 32 x 32 x 2 takes 64 for twice the work),
+// and bf16's 32 x 32 form reaches 2.1 PFLOP/s where its 16 x 16 form reaches
+// only 1.2; fp32's fine 16 x 16 tiles fit ViT-Tiny's 192- and 197-wide shapes. Lane l reads one 16-byte fragment per operand per k-block:
 // row l % E of its operand and k chunk l / E, so a k-block is 16 consecutive
 // k for both types. bf16 feeds the chunk to one MFMA. fp32 feeds element s of
 // the chunk to the s-th of four MFMAs, so MFMA s of a k-block sums
@@ -110,15 +111,15 @@ __device__ __forceinline__ Offsets entry_offsets(const GemmArgs& args, int entry
 }
 
 /// alpha, bias, the optional addend, GELU: everything of the epilogue before
-/// the store.
-__device__ __forceinline__ float epilogue_value(float sum, const float* bias, int row, int column,
-                                                const GemmArgs& args) {
+/// the store, with the bias term already loaded (@p with_bias false: none).
+__device__ __forceinline__ float epilogue_value(float sum, bool with_bias, float bias_value, int row,
+                                                int column, const GemmArgs& args) {
     // alpha * sum and each addition round on their own (no fused multiply-add),
     // the reference's order, in every GEMM kernel alike.
 #pragma clang fp contract(off)
     float value = args.alpha * sum;
-    if (bias != nullptr) {
-        value += bias[column];
+    if (with_bias) {
+        value += bias_value;
     }
     if (args.addend != nullptr) {
         value += args.addend[static_cast<std::int64_t>(row) * args.ld_addend + column];
@@ -127,6 +128,12 @@ __device__ __forceinline__ float epilogue_value(float sum, const float* bias, in
         value = gelu(value);
     }
     return value;
+}
+
+__device__ __forceinline__ float epilogue_value(float sum, const float* bias, int row, int column,
+                                                const GemmArgs& args) {
+    return epilogue_value(sum, bias != nullptr, bias != nullptr ? bias[column] : 0.0F, row, column,
+                          args);
 }
 
 // -- operand loads ------------------------------------------------------------
@@ -183,12 +190,23 @@ __device__ __forceinline__ Vec16 load_chunk_scalar(const T* matrix, int ld, int 
     return v;
 }
 
+/// The accumulating epilogue's C + value, rounded on its own: the add never
+/// fuses with the multiply that ends the GELU before it, in any kernel, so
+/// every kernel gives the same bits.
+__device__ __forceinline__ float add_unfused(float c, float value) {
+#pragma clang fp contract(off)
+    return c + value;
+}
+
 /// Stores four consecutive results (C = value, or C += value), 16 bytes for
 /// fp32 and 8 for bf16; @p p is aligned to that size.
 __device__ __forceinline__ void store4(float* p, const float (&value)[4], bool accumulate) {
     floatx4 v{value[0], value[1], value[2], value[3]};
     if (accumulate) {
-        v += *reinterpret_cast<const floatx4*>(p);
+        const floatx4 old = *reinterpret_cast<const floatx4*>(p);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            v[r] = add_unfused(old[r], v[r]);
     }
     *reinterpret_cast<floatx4*>(p) = v;
 }
@@ -197,10 +215,10 @@ __device__ __forceinline__ void store4(std::uint16_t* p, const float (&value)[4]
     float v[4] = {value[0], value[1], value[2], value[3]};
     if (accumulate) {
         const uint2 old = *reinterpret_cast<const uint2*>(p);
-        v[0] = bf16_to_float(static_cast<std::uint16_t>(old.x & 0xFFFFU)) + v[0];
-        v[1] = bf16_to_float(static_cast<std::uint16_t>(old.x >> 16)) + v[1];
-        v[2] = bf16_to_float(static_cast<std::uint16_t>(old.y & 0xFFFFU)) + v[2];
-        v[3] = bf16_to_float(static_cast<std::uint16_t>(old.y >> 16)) + v[3];
+        v[0] = add_unfused(bf16_to_float(static_cast<std::uint16_t>(old.x & 0xFFFFU)), v[0]);
+        v[1] = add_unfused(bf16_to_float(static_cast<std::uint16_t>(old.x >> 16)), v[1]);
+        v[2] = add_unfused(bf16_to_float(static_cast<std::uint16_t>(old.y & 0xFFFFU)), v[2]);
+        v[3] = add_unfused(bf16_to_float(static_cast<std::uint16_t>(old.y >> 16)), v[3]);
     }
     uint2 bits;
     bits.x = static_cast<std::uint32_t>(float_to_bf16(v[0])) |
@@ -555,7 +573,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(MinWav
                             if (col + r < args.n) {
                                 float v = value[r];
                                 if (args.accumulate) {
-                                    v = Elem<T>::load(c_row + col + r) + v;
+                                    v = add_unfused(Elem<T>::load(c_row + col + r), v);
                                 }
                                 Elem<T>::store(c_row + col + r, v);
                             }

@@ -1,0 +1,82 @@
+"""The resident-panel fp32 GEMM (a B panel held in LDS for the whole of K, A
+fragments loaded straight into the MFMA layout), which tall single fp32
+products with B as [N, K] take: the model's linear layers at batch 32.
+
+Its results must be bitwise those of the LDS-tiled kernel that small problems
+take: both run v_mfma_f32_16x16x4_f32 over the same k-blocks in the same order
+and apply alpha, the bias and GELU without fusing them. Each case launches a
+problem large enough for the panel kernel (at least eight wavefront items per
+compute unit; outputs that are not accumulated into start as NaN), then the
+same rows in launches of 197 rows, small enough for the tiled kernel, and
+requires equality bit for bit; one block of rows is also judged against the
+oracle.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import to_device, to_host
+from numerics import require_close, require_close_scaled, require_exact
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # m, n, k, bias, gelu, accumulate, alpha, lda pad, ldc pad
+    (6304, 768, 192, True, True, False, 1.0, 0, 0),      # ViT-Tiny FC1 + GELU
+    (6304, 576, 192, True, False, False, 1.0, 0, 0),     # QKV
+    (6304, 192, 192, True, False, True, 1.0, 0, 0),      # projection into the residual
+    (6304, 192, 768, True, False, True, 1.0, 0, 0),      # FC2 into the residual
+    (4099, 196, 180, False, True, True, 0.75, 8, 4),     # M, N and K tails, GELU + accumulate
+    (5000, 580, 740, True, True, False, -1.25, 4, 0),    # 48 k-blocks with a K tail, alpha
+    (4111, 392, 64, True, False, False, 2.0, 0, 12),     # K = 64: 12 k-blocks, 8 of them zero
+]
+
+
+@pytest.mark.parametrize("m,n,k,with_bias,gelu,accumulate,alpha,lda_pad,ldc_pad", CASES)
+def test_panel_equals_the_tiled_kernel(cuvit, oracle, device, m, n, k, with_bias, gelu, accumulate,
+                                       alpha, lda_pad, ldc_pad):
+    lda, ldc = k + lda_pad, n + ldc_pad
+    g = oracle.generator(m + 3 * n + 7 * k)
+    a = g.normal(m * lda)
+    w = g.normal(n * k, 0.0, 0.05)
+    bias = g.normal(n, 0.0, 0.5) if with_bias else None
+    start_c = g.normal(m * ldc) if accumulate else np.full(m * ldc, np.nan, np.float32)
+    da, dw = to_device(a, device), to_device(w, device)
+    dbias = to_device(bias, device) if with_bias else None
+
+    def problem(rows):
+        p = cuvit.gemm_problem(rows, n, k, cuvit.TRANSPOSED)
+        p.alpha = alpha
+        p.lda, p.ldc = lda, ldc
+        p.epilogue.gelu = int(gelu)
+        p.epilogue.accumulate = int(accumulate)
+        return p
+
+    c = to_device(start_c, device)
+    cuvit.gemm(da, dw, dbias, c, problem(m))
+    full = to_host(c).reshape(m, ldc)[:, :n]
+    rows = 197
+    for start in range(0, m, rows):
+        count = min(rows, m - start)
+        part = to_device(start_c[start * ldc:(start + count) * ldc], device)
+        cuvit.gemm(da[start * lda:], dw, dbias, part, problem(count))
+        require_exact(to_host(part).reshape(count, ldc)[:, :n], full[start:start + count],
+                      f"rows {start}..{start + count} differ from launches of {rows} rows")
+    last = m - 64
+    sample = np.ascontiguousarray(a.reshape(m, lda)[last:, :k])
+    pre = oracle.gemm_transposed(sample, w, bias, 64, n, k, alpha)
+    scale = oracle.term_magnitudes(sample, w, 64, n, k, True, alpha)
+    value = oracle.gelu(pre) if gelu else pre
+    existing = start_c.reshape(m, ldc)[last:, :n]
+    if gelu:
+        expected = existing + value if accumulate else value
+        require_close(full[last:], expected, "last 64 rows against the oracle", 1.0e-4, 1.0e-5)
+    else:
+        expected = existing + value if accumulate else value
+        require_close_scaled(full[last:], expected, scale, "last 64 rows against the oracle",
+                             1.0e-6, 1.0e-5)
+    padding = to_host(c).reshape(m, ldc)[:, n:]
+    require_exact(padding, start_c.reshape(m, ldc)[:, n:], "the columns past N changed")
