@@ -142,7 +142,7 @@ std::int64_t tile_count(const GemmArgs& args, int bm, int bn) {
 } // namespace
 
 /// The resident-panel kernel (gemm_panel.hpp) for a problem it covers: one
-/// batch entry, B as [N, K], K rounded up to 64 equal to 16 KB, vector A and
+/// batch entry, B as [N, K], K equal to 16 KB, vector A and
 /// B, C written in 16-byte runs (N, ldc multiples of 4, C 16-byte aligned), no
 /// addend, every operand within one descriptor's span, and at least eight
 /// wavefront items per compute unit. Returns hipErrorNotSupported otherwise.
@@ -154,7 +154,7 @@ hipError_t launch_panel(const float* a, const float* b, const float* bias, float
     const std::int64_t panels = (args.n + BN - 1) / BN;
     const bool eligible =
         args.count == 1 && args.transposed && args.addend == nullptr &&
-        (args.k + 63) / 64 * 4 == KB && vector_operand(a, args.lda, args.k, 0, 0, false) &&
+        args.k == 16 * KB && vector_operand(a, args.lda, args.k, 0, 0, false) &&
         vector_operand(b, args.ldb, args.k, 0, 0, false) && vector_output(c, args) && aligned16(c) &&
         args.n % 4 == 0 && static_cast<std::int64_t>(args.m) * args.lda * 4 < gemm::kMaxSpan &&
         static_cast<std::int64_t>(args.m) * args.ldc * 4 < gemm::kMaxSpan &&
@@ -205,13 +205,20 @@ hipError_t gemm_f32(const float* a, const float* b, const float* bias, float* c,
                     const GemmArgs& args, hipStream_t stream) {
     // Tall single products with B as [N, K] (the model's linear layers): the
     // resident-panel kernel, bitwise equal to the tiles below. Measured at
-    // ViT-Tiny batch 32 (6304 rows): QKV 21.4 -> 18.2 us, projection 10.7 ->
-    // 8.9, FC1 + GELU 27.9 -> 25.2, FC2 25.7 -> 24.7.
-    if (const hipError_t panel = launch_panel<12, 64, 2, 4, 8>(a, b, bias, c, args, stream);
-        panel != hipErrorNotSupported) {
+    // ViT-Tiny batch 32 (6304 rows), against the tiled kernel: QKV 21.4 ->
+    // 17.8 us, FC1 + GELU 27.9 -> 24.2, projection 10.7 -> 8.4, FC2 25.7 ->
+    // 22.7. Wide panels with three wavefronts per SIMD suit the wide outputs,
+    // 32-column panels the 192-wide ones.
+    if (args.n >= 512) {
+        if (const hipError_t panel = launch_panel<12, 64, 2, 4, 12>(a, b, bias, c, args, stream);
+            panel != hipErrorNotSupported) {
+            return panel;
+        }
+    } else if (const hipError_t panel = launch_panel<12, 32, 2, 4, 8>(a, b, bias, c, args, stream);
+               panel != hipErrorNotSupported) {
         return panel;
     }
-    if (const hipError_t panel = launch_panel<48, 32, 2, 6, 8>(a, b, bias, c, args, stream);
+    if (const hipError_t panel = launch_panel<48, 32, 2, 4, 12>(a, b, bias, c, args, stream);
         panel != hipErrorNotSupported) {
         return panel;
     }

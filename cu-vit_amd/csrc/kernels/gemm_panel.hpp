@@ -12,38 +12,44 @@
 //
 // Same arithmetic as gemm_kernel<float>: lane l holds row l % 16 of A and of
 // the panel at k chunk l / 16, k-blocks of 16 are walked in ascending order
-// over K rounded up to a multiple of 64, and element s of a fragment feeds the
+// over K (a multiple of 64 here, as the tiled kernel rounds it), and element s
+// of a fragment feeds the
 // s-th of four v_mfma_f32_16x16x4_f32 (B fragment as the first operand). So
 // every accumulator sees the same MFMAs with the same operands in the same
 // order as in the LDS-tiled kernel, and the two give bitwise equal results;
 // the epilogue (alpha, bias, GELU, store or accumulate) is the same function.
-// Elements past M, N or K read as zero; results past M are not stored, and N
-// is a multiple of 4 so a run of four columns is all in or all out.
+// Rows past M and panel rows past N read as zero; results past M are not
+// stored, and N is a multiple of 4 so a run of four columns is all in or all
+// out. An out-of-range offset past kOutside plus a group's 64-byte steps
+// stays past the buffer resource's record count, so it reads zero.
 #pragma once
 
 #include "gemm_kernel.hpp"
 
 namespace cuvit::detail::gemm {
 
-/// @tparam KB k-blocks of 16 walked (K rounded up to a multiple of 64, / 16)
+/// @tparam KB k-blocks of 16 (K = 16 KB, a multiple of 64)
 /// @tparam BN panel width (columns of C, rows of B)
-/// @tparam TN 16-column MFMA tiles per wavefront item
+/// @tparam TN 16-column MFMA tiles of a full wavefront item (even: a half
+///         item has TN / 2)
 /// @tparam KG k-blocks of A per register group
-/// @tparam W wavefronts per workgroup
+/// @tparam W wavefronts per workgroup (a multiple of the 4 SIMDs)
 template <int KB, int BN, int TN, int KG, int W> struct PanelShape {
     static_assert(KB % 4 == 0, "K walked in spans of 64");
-    static_assert(BN % (16 * TN) == 0, "a panel is whole wavefront items wide");
-    static constexpr int kParts = BN / (16 * TN); // wavefronts sharing one row tile
-    static_assert(W % kParts == 0, "every wavefront keeps one column part");
-    static constexpr int kRowStride = W / kParts; // row tiles between a wavefront's items
+    static_assert(TN % 2 == 0, "a full item splits into two halves");
+    static_assert(BN % (16 * TN) == 0, "a panel is whole items wide");
+    static constexpr int kParts = BN / (16 * TN); // full items across the panel
+    static_assert(W % 4 == 0, "the same number of wavefronts on every SIMD");
+    static constexpr int kPerSimd = W / 4;
     static_assert(KB % KG == 0, "register groups split K evenly");
     static constexpr int kGroups = KB / KG;
-    static_assert(KG >= TN, "a step has a k-block for each epilogue slice");
     /// Floats per LDS panel row: 16 KB plus a 16-byte pad, so that the 16
     /// lanes reading one fragment column (16 rows, same k) hit 16 different
     /// bank quads (16 KB floats is a multiple of 64 banks).
     static constexpr int kPitch = 16 * KB + 4;
-    static constexpr std::size_t kLdsBytes = static_cast<std::size_t>(BN) * kPitch * sizeof(float);
+    static constexpr int kPanelFloats = BN * kPitch;
+    /// The panel, then the panel's BN bias values.
+    static constexpr std::size_t kLdsBytes = static_cast<std::size_t>(kPanelFloats + BN) * sizeof(float);
     static constexpr int kThreads = kWave * W;
     static constexpr int kChunks = BN * 4 * KB; // 16-byte chunks of the panel
     static constexpr int kChunksPerThread = (kChunks + kThreads - 1) / kThreads;
@@ -52,6 +58,13 @@ template <int KB, int BN, int TN, int KG, int W> struct PanelShape {
 /// @p groups row-tile ranges per panel: workgroup x computes panel x / groups
 /// over range x % groups. The epilogue's parts are compile-time; there is no
 /// addend, and kAlpha false means alpha is 1 (1 * x is x, bit for bit).
+///
+/// Work split. A workgroup's R row tiles make U = R * kParts full items
+/// (16 x 16 TN). The first 4 floor(U / 4) go round robin to the four SIMDs,
+/// the rest are cut into half items (16 x 8 TN) dealt the same way, so no
+/// SIMD carries more than half an item beyond another: the MFMA pipe is the
+/// bound, and a whole item's difference would idle three SIMDs for its
+/// length. The wavefronts of a SIMD take its items in turn.
 template <int KB, int BN, int TN, int KG, int W, bool kAlpha, bool kBias, bool kGelu, bool kAccumulate>
 __global__ __launch_bounds__(kWave * W) void gemm_panel_kernel(const float* __restrict__ a,
                                                              const float* __restrict__ b,
@@ -59,8 +72,10 @@ __global__ __launch_bounds__(kWave * W) void gemm_panel_kernel(const float* __re
                                                              float* c, GemmArgs args, int groups) {
     using S = PanelShape<KB, BN, TN, KG, W>;
     constexpr int G = S::kGroups;
+    constexpr int kHalf = TN / 2;
     extern __shared__ Vec16 lds_vectors[];
     float* const panel = reinterpret_cast<float*>(lds_vectors);
+    float* const panel_bias = panel + S::kPanelFloats;
 
     const int t = threadIdx.x;
     const int lane = lane_id();
@@ -72,10 +87,33 @@ __global__ __launch_bounds__(kWave * W) void gemm_panel_kernel(const float* __re
     const int group = static_cast<int>(blockIdx.x) % groups;
     const int col0 = panel_index * BN;
     const int tiles_m = (args.m + 15) / 16;
-    const int tile_hi = split_point(tiles_m, groups, group + 1);
-    const int part = wave % S::kParts;
-    const int first_tile = split_point(tiles_m, groups, group) + wave / S::kParts;
-    const int tiles = first_tile < tile_hi ? (tile_hi - first_tile + S::kRowStride - 1) / S::kRowStride : 0;
+    const int tile_lo = split_point(tiles_m, groups, group);
+    const int units = (split_point(tiles_m, groups, group + 1) - tile_lo) * S::kParts;
+    const int whole = units / 4 * 4;           // full items, dealt four at a time
+    const int halves = 2 * (units - whole);    // the rest, as half items
+    const int simd = wave % 4;
+    const int slot = wave / 4;
+    const int full_per_simd = whole / 4;
+    const int simd_items = full_per_simd + (simd < halves ? (halves - simd + 3) / 4 : 0);
+    const int items = slot < simd_items ? (simd_items - slot + S::kPerSimd - 1) / S::kPerSimd : 0;
+
+    // Item n of this wavefront: its row tile, its first column within the
+    // panel, and whether it is a full item.
+    struct Item {
+        int tile;
+        int column;
+        bool full;
+    };
+    auto item = [&](int n) -> Item {
+        const int e = slot + S::kPerSimd * n;
+        if (e < full_per_simd) {
+            const int u = simd + 4 * e;
+            return {tile_lo + u / S::kParts, (u % S::kParts) * 16 * TN, true};
+        }
+        const int q = simd + 4 * (e - full_per_simd);
+        const int u = whole + q / 2;
+        return {tile_lo + u / S::kParts, (u % S::kParts) * 16 * TN + (q % 2) * 16 * kHalf, false};
+    };
 
     // Panel loads: B rows col0 .. col0 + BN, k 0 .. 16 KB; zero past N and K.
     const auto b_resource = buffer_resource(b + static_cast<std::int64_t>(col0) * args.ldb);
@@ -90,27 +128,32 @@ __global__ __launch_bounds__(kWave * W) void gemm_panel_kernel(const float* __re
             staged[p] = buffer_load16(b_resource, chunk_offset<float>(row, b_rows, args.ldb, k, args.k));
         }
     }
+    // The panel's bias (zero past N, or without a bias).
+    Vec16 staged_bias{{0U, 0U, 0U, 0U}};
+    if (kBias && t < BN / 4) {
+        staged_bias = buffer_load16(buffer_resource(bias), col0 + 4 * t < args.n
+                                                               ? static_cast<unsigned int>((col0 + 4 * t) * 4)
+                                                               : kOutside);
+    }
 
-    // This lane's row of the wavefront's @p n-th tile.
-    auto tile_row = [&](int n) { return (first_tile + n * S::kRowStride) * 16 + fragment_row; };
-
-    // A fragments of group @p g of the wavefront's @p n-th tile; a tile past
-    // the wavefront's last reads nothing.
+    // A fragments of group @p g of row tile @p tile; an item past the
+    // wavefront's last (@p live false) or a row past M reads nothing. K is
+    // exactly 16 KB, so every k-block is inside; the k-blocks of a group sit
+    // 64 bytes apart, which the loads take as immediate offsets.
     const auto a_resource = buffer_resource(a);
-    auto fetch = [&](Vec16 (&ra)[KG], int n, int g) {
-        const int row = tile_row(n);
-        const int k0 = 16 * KG * g + 4 * fragment_chunk;
-        const bool live = n < tiles && row < args.m;
-        const unsigned int base = static_cast<unsigned int>((row * args.lda + k0) * 4);
+    auto fetch = [&](Vec16 (&ra)[KG], int tile, bool live, int g) {
+        const int row = tile * 16 + fragment_row;
+        const unsigned int base =
+            live && row < args.m ? static_cast<unsigned int>((row * args.lda + 16 * KG * g + 4 * fragment_chunk) * 4)
+                                 : kOutside;
 #pragma unroll
         for (int kb = 0; kb < KG; ++kb) {
-            const bool inside = live && k0 + 16 * kb < args.k;
-            ra[kb] = buffer_load16(a_resource, inside ? base + 64U * kb : kOutside);
+            ra[kb] = buffer_load16(a_resource, base + 64U * kb);
         }
     };
 
     Vec16 ra[2][KG];
-    fetch(ra[0], 0, 0);
+    fetch(ra[0], item(0).tile, items > 0, 0);
 
 #pragma unroll
     for (int p = 0; p < S::kChunksPerThread; ++p) {
@@ -120,63 +163,72 @@ __global__ __launch_bounds__(kWave * W) void gemm_panel_kernel(const float* __re
             store16(panel + row * S::kPitch + 4 * (q % (4 * KB)), staged[p]);
         }
     }
-
-    // The bias of the wavefront's columns, loaded once: lane l's column run
-    // of tile j starts at column(j).
-    auto column = [&](int j) { return col0 + part * 16 * TN + 16 * j + 4 * fragment_chunk; };
-    float bias_value[TN][4];
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            bias_value[j][r] = kBias && column(j) < args.n ? bias[column(j) + r] : 0.0F;
-
+    if (t < BN / 4) {
+        store16(panel_bias + 4 * t, staged_bias);
+    }
     __syncthreads();
 
     // A lane with nothing to store (row past M, columns past N) stores to an
     // offset the buffer resource drops, so the epilogue has no branch.
     const auto c_resource = buffer_resource(c);
-    auto c_offset = [&](int row, int j) {
-        return row < args.m && column(j) < args.n ? static_cast<unsigned int>((row * args.ldc + column(j)) * 4)
-                                                  : kOutside;
+    auto c_offset = [&](int row, int column) {
+        return row < args.m && column < args.n ? static_cast<unsigned int>((row * args.ldc + column) * 4)
+                                               : kOutside;
     };
 
-    const float* const fragments = panel + (part * 16 * TN + fragment_row) * S::kPitch + 4 * fragment_chunk;
     floatx4 acc[TN];
     floatx4 old[TN];
 
-    // MFMAs of group @p g over the A fragments in @p ra. B fragments are read
-    // one k-block ahead of their MFMAs, two sets live: the schedule barrier
-    // keeps the compiler from hoisting every k-block's LDS reads to the top,
-    // which would hold TN * KG fragments at once.
-    auto multiply = [&](const Vec16 (&fa)[KG], int g) {
-        const float* const base = fragments + 16 * KG * g;
-        Vec16 fb[2][TN];
+    // MFMAs of group @p g over the A fragments in @p fa, for the Tiles
+    // 16-column tiles from panel column @p column. B fragments are read
+    // kLead k-blocks ahead of their MFMAs (kLead + 1 sets live); the schedule
+    // barrier keeps the compiler from hoisting every k-block's LDS reads to
+    // the top.
+    constexpr int kLead = KG > 2 ? 2 : 1;
+    auto multiply = [&](auto tiles, const Vec16 (&fa)[KG], int g, int column) {
+        constexpr int Tiles = decltype(tiles)::value;
+        const float* const base = panel + (column + fragment_row) * S::kPitch + 16 * KG * g + 4 * fragment_chunk;
+        Vec16 fb[kLead + 1][Tiles];
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-            fb[0][j] = load16(base + j * 16 * S::kPitch);
+        for (int kb = 0; kb < kLead; ++kb)
+#pragma unroll
+            for (int j = 0; j < Tiles; ++j)
+                fb[kb][j] = load16(base + j * 16 * S::kPitch + 16 * kb);
 #pragma unroll
         for (int kb = 0; kb < KG; ++kb) {
-            if (kb + 1 < KG) {
+            if (kb + kLead < KG) {
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    fb[(kb + 1) & 1][j] = load16(base + j * 16 * S::kPitch + 16 * (kb + 1));
+                for (int j = 0; j < Tiles; ++j)
+                    fb[(kb + kLead) % (kLead + 1)][j] = load16(base + j * 16 * S::kPitch + 16 * (kb + kLead));
             }
 #pragma unroll
             for (int s = 0; s < 4; ++s)
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
+                for (int j = 0; j < Tiles; ++j)
                     acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                        __uint_as_float(fb[kb & 1][j].w[s]), __uint_as_float(fa[kb].w[s]),
+                        __uint_as_float(fb[kb % (kLead + 1)][j].w[s]), __uint_as_float(fa[kb].w[s]),
                         g == 0 && kb == 0 && s == 0 ? floatx4{0.F, 0.F, 0.F, 0.F} : acc[j], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
-    auto finish = [&](int n) {
-        const int row = tile_row(n);
+    auto load_old = [&](auto tiles, int row, int column) {
+        constexpr int Tiles = decltype(tiles)::value;
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
+        for (int j = 0; j < Tiles; ++j)
+            old[j] = __builtin_bit_cast(
+                floatx4, buffer_load16(c_resource, c_offset(row, col0 + column + 16 * j + 4 * fragment_chunk)));
+    };
+
+    auto finish = [&](auto tiles, int row, int column) {
+        constexpr int Tiles = decltype(tiles)::value;
+#pragma unroll
+        for (int j = 0; j < Tiles; ++j) {
+            const int within = column + 16 * j + 4 * fragment_chunk;
+            floatx4 bias_value{0.F, 0.F, 0.F, 0.F};
+            if constexpr (kBias) {
+                bias_value = __builtin_bit_cast(floatx4, load16(panel_bias + within));
+            }
             floatx4 value;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -188,7 +240,7 @@ __global__ __launch_bounds__(kWave * W) void gemm_panel_kernel(const float* __re
                     v = args.alpha * v;
                 }
                 if constexpr (kBias) {
-                    v += bias_value[j][r];
+                    v += bias_value[r];
                 }
                 if constexpr (kGelu) {
                     v = gelu(v);
@@ -200,37 +252,54 @@ __global__ __launch_bounds__(kWave * W) void gemm_panel_kernel(const float* __re
                 for (int r = 0; r < 4; ++r)
                     value[r] = add_unfused(old[j][r], value[r]);
             }
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, value), c_resource, c_offset(row, j), 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, value), c_resource,
+                                                   c_offset(row, col0 + within), 0, 0);
         }
     };
 
-    // Tile n, its groups in order; step s = G n + g uses register set s % 2,
-    // and the set it frees is refilled for step s + 2. Two tiles per trip
+    // Item n, its groups in order; step s = G n + g uses register set s % 2,
+    // and the set it frees is refilled for step s + 1. Two items per trip
     // keep every set index a compile-time constant.
-    auto tile = [&](int n, int parity) {
+    auto run_item = [&](int n, int parity) {
+        const Item it = item(n);
+        const Item next = item(n + 1);
+        const int row = it.tile * 16 + fragment_row;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const int set = (parity + g) & 1;
             if constexpr (kAccumulate) {
                 if (g == G - 1) {
                     // the old C, loaded ahead of the last group's MFMAs
-                    const int row = tile_row(n);
-#pragma unroll
-                    for (int j = 0; j < TN; ++j)
-                        old[j] = __builtin_bit_cast(floatx4, buffer_load16(c_resource, c_offset(row, j)));
+                    if (it.full) {
+                        load_old(std::integral_constant<int, TN>{}, row, it.column);
+                    } else {
+                        load_old(std::integral_constant<int, kHalf>{}, row, it.column);
+                    }
                 }
             }
             // step s + 1 into the other set, then this step's MFMAs
-            fetch(ra[set ^ 1], g + 1 < G ? n : n + 1, g + 1 < G ? g + 1 : 0);
-            multiply(ra[set], g);
+            if (g + 1 < G) {
+                fetch(ra[set ^ 1], it.tile, true, g + 1);
+            } else {
+                fetch(ra[set ^ 1], next.tile, n + 1 < items, 0);
+            }
+            if (it.full) {
+                multiply(std::integral_constant<int, TN>{}, ra[set], g, it.column);
+            } else {
+                multiply(std::integral_constant<int, kHalf>{}, ra[set], g, it.column);
+            }
         }
-        finish(n);
+        if (it.full) {
+            finish(std::integral_constant<int, TN>{}, row, it.column);
+        } else {
+            finish(std::integral_constant<int, kHalf>{}, row, it.column);
+        }
     };
 
-    for (int n = 0; n < tiles; n += 2) {
-        tile(n, 0);
-        if (n + 1 < tiles) {
-            tile(n + 1, G & 1);
+    for (int n = 0; n < items; n += 2) {
+        run_item(n, 0);
+        if (n + 1 < items) {
+            run_item(n + 1, G & 1);
         }
     }
 }

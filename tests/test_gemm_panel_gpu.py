@@ -5,8 +5,8 @@ products with B as [N, K] take: the model's linear layers at batch 32.
 Its results must be bitwise those of the LDS-tiled kernel that small problems
 take: both run v_mfma_f32_16x16x4_f32 over the same k-blocks in the same order
 and apply alpha, the bias and GELU without fusing them. Each case launches a
-problem large enough for the panel kernel (at least eight wavefront items per
-compute unit; outputs that are not accumulated into start as NaN), then the
+problem the panel kernel takes (K of 192 or 768, at least eight wavefront
+items per compute unit; outputs that are not accumulated into start as NaN), then the
 same rows in launches of 197 rows, small enough for the tiled kernel, and
 requires equality bit for bit; one block of rows is also judged against the
 oracle.
@@ -29,9 +29,9 @@ CASES = [
     (6304, 576, 192, True, False, False, 1.0, 0, 0),     # QKV
     (6304, 192, 192, True, False, True, 1.0, 0, 0),      # projection into the residual
     (6304, 192, 768, True, False, True, 1.0, 0, 0),      # FC2 into the residual
-    (4099, 196, 180, False, True, True, 0.75, 8, 4),     # M, N and K tails, GELU + accumulate
-    (5000, 580, 740, True, True, False, -1.25, 4, 0),    # 48 k-blocks with a K tail, alpha
-    (4111, 392, 64, True, False, False, 2.0, 0, 12),     # K = 64: 12 k-blocks, 8 of them zero
+    (4099, 196, 192, False, True, True, 0.75, 8, 4),     # M and N tails, GELU + accumulate, alpha
+    (5000, 580, 768, True, True, False, -1.25, 4, 0),    # 48 k-blocks, N tail, alpha
+    (4111, 392, 192, True, False, False, 2.0, 0, 12),    # a partial last panel, padded C rows
 ]
 
 
