@@ -116,16 +116,17 @@ __device__ __forceinline__ Vec16 value_fragment(const std::uint16_t* values, int
     return fragment;
 }
 
-/// 16 bytes at @p element of @p base, or zero when @p inside is false.
-__device__ __forceinline__ Vec16 load_or_zero(const std::uint16_t* base, std::int64_t element,
+/// 16 bytes at @p element of the pair's packed projection, through the
+/// buffer resource @p resource (based at that element 0), or zero when
+/// @p inside is false: the offset is then one the resource drops, so the load
+/// needs no branch. Element offsets stay far inside 32 bits (at most 256
+/// tokens of 3 * heads * 64 elements).
+__device__ __forceinline__ Vec16 load_or_zero(__amdgpu_buffer_rsrc_t resource, std::int64_t element,
                                               bool inside) {
-    return inside ? load16(base + element) : Vec16{{0U, 0U, 0U, 0U}};
+    return gemm::buffer_load16(resource, inside ? static_cast<unsigned int>(element * 2) : gemm::kOutside);
 }
 
 __device__ __forceinline__ float exchange(float value) { return __shfl_xor(value, 32, kWave); }
-__device__ __forceinline__ std::uint32_t exchange(std::uint32_t value) {
-    return static_cast<std::uint32_t>(__shfl_xor(static_cast<int>(value), 32, kWave));
-}
 
 __device__ __forceinline__ std::uint32_t pack_bf16(float low, float high) {
     return pack_bf16x2(low, high);
@@ -178,11 +179,12 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
     auto load_direct = [&](const PairBases& b, int buffer) {
         std::uint16_t* const values = lds + buffer * kBufferElements;
         std::uint16_t* const keys = values + kPadded * kHeadDim;
+        const auto resource = gemm::buffer_resource(b.k);
         for (int c = threadIdx.x; c < kPadded * kChunks; c += blockDim.x) {
             const int key = c / kChunks;
             const int d0 = 8 * (c % kChunks);
-            const Vec16 v = load_or_zero(b.v, key * qkv_row + d0, key < tokens);
-            const Vec16 k = load_or_zero(b.k, key * qkv_row + d0, key < tokens);
+            const Vec16 v = load_or_zero(resource, key * qkv_row + d0 + embed, key < tokens);
+            const Vec16 k = load_or_zero(resource, key * qkv_row + d0, key < tokens);
             store16(values + value_slot(key, d0), v);
             store16(keys + key * kKeyPitch + d0, k);
         }
@@ -191,6 +193,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
     // thread (c % threads)'s element c / threads; V's chunks first.
     Vec16 ahead[Chunks > 0 ? Chunks : 1];
     auto prefetch = [&](const PairBases& b) {
+        // V sits embed elements after K in every token's row.
+        const auto resource = gemm::buffer_resource(b.k);
 #pragma unroll
         for (int i = 0; i < Chunks; ++i) {
             const int c = static_cast<int>(threadIdx.x) + i * static_cast<int>(blockDim.x);
@@ -198,7 +202,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
             const int cc = is_key ? c - kPadded * kChunks : c;
             const int key = cc / kChunks;
             const int d0 = 8 * (cc % kChunks);
-            ahead[i] = load_or_zero(is_key ? b.k : b.v, key * qkv_row + d0,
+            ahead[i] = load_or_zero(resource, key * qkv_row + d0 + (is_key ? 0 : embed),
                                     c < 2 * kPadded * kChunks && key < tokens);
         }
     };
@@ -222,62 +226,82 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
         }
     };
 
+    // This wavefront's query tile, the same in every pair; its Q fragments
+    // (16 contiguous bytes of row query, k chunk 8 half) straight from global
+    // memory, the next pair's loaded while the current one is worked on.
+    const int query0 = (static_cast<int>(blockIdx.x) * waves + wave) * kEdge;
+    const int query = query0 + row;
+    auto load_queries = [&](const PairBases& b, Vec16 (&q)[kHeadDim / kKBlock]) {
+        const auto resource = gemm::buffer_resource(b.q);
+#pragma unroll
+        for (int kb = 0; kb < kHeadDim / kKBlock; ++kb) {
+            q[kb] = load_or_zero(resource, query * qkv_row + kb * kKBlock + chunk, query < tokens);
+        }
+    };
+
     int pair = static_cast<int>(blockIdx.y);
     int buffer = 0;
+    Vec16 q[kHeadDim / kKBlock];
+    Vec16 q_ahead[kHeadDim / kKBlock];
     load_direct(pair_bases(qkv, pair, heads, tokens), 0);
+    load_queries(pair_bases(qkv, pair, heads, tokens), q);
     __syncthreads();
     for (;;) {
     const int next = pair + static_cast<int>(gridDim.y);
     const bool more = Chunks > 0 && next < pairs;
     if (more) {
         prefetch(pair_bases(qkv, next, heads, tokens));
+        load_queries(pair_bases(qkv, next, heads, tokens), q_ahead);
     }
     const PairBases bases = pair_bases(qkv, pair, heads, tokens);
-    const std::uint16_t* const q_base = bases.q;
     const int image = bases.image;
     const int head = bases.head;
     const std::uint16_t* const values = lds + buffer * kBufferElements;
     const std::uint16_t* const keys = values + kPadded * kHeadDim;
-    const int query0 = (static_cast<int>(blockIdx.x) * waves + wave) * kEdge;
     if (query0 < tokens) {
-    const int query = query0 + row;
 
     // Logits tiles: the GEMM's MFMA and operand roles, alpha * sum rounded
     // to bf16 as the GEMM stores it, then read back as the softmax reads it.
-    Vec16 q[kHeadDim / kKBlock];
-#pragma unroll
-    for (int kb = 0; kb < kHeadDim / kKBlock; ++kb) {
-        q[kb] = load_or_zero(q_base, query * qkv_row + kb * kKBlock + chunk, query < tokens);
-    }
+    // The first k-block's MFMA takes its zero accumulator as an inline
+    // constant (the same +0 the GEMM starts from, without 16 moves a tile).
     Acc x[KT];
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
         const int key = kt * kEdge + row;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            x[kt][i] = 0.F;
-        }
-#pragma unroll
         for (int kb = 0; kb < kHeadDim / kKBlock; ++kb) {
             const Vec16 k = load16(keys + key * kKeyPitch + kb * kKBlock + chunk);
-            Bf16Mma::run(x[kt], k, q[kb]);
+            x[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(gemm::bf16x8, k),
+                                                           __builtin_bit_cast(gemm::bf16x8, q[kb]),
+                                                           kb == 0 ? Acc{} : x[kt], 0, 0, 0);
         }
     }
 
-    // Row max over the valid keys (exact in any order).
+    // alpha * sum rounded to bf16, two logits per conversion (the same
+    // rounding as one at a time). The row max over the valid keys is exact
+    // in any order, and rounding to nearest never reverses an order, so the
+    // max of the rounded logits is the rounded max of the unrounded ones:
+    // it is taken over the products, which need no canonicalizing.
     float maximum = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
+            x[kt][i] = scale * x[kt][i];
             const int key = kt * kEdge + Bf16Mma::column(lane, i / 4) + i % 4;
-            x[kt][i] = bf16_to_float(float_to_bf16(scale * x[kt][i]));
             // Only the last key tile holds keys past the tokens.
             if (kt < KT - 1 || key < tokens) {
                 maximum = fmaxf(maximum, x[kt][i]);
             }
         }
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+            const std::uint32_t bits = pack_bf16x2(x[kt][i], x[kt][i + 1]);
+            x[kt][i] = __uint_as_float(bits << 16);
+            x[kt][i + 1] = __uint_as_float(bits & 0xFFFF0000U);
+        }
     }
+    maximum = bf16_to_float(float_to_bf16(maximum));
     maximum = fmaxf(maximum, exchange(maximum));
 
     // Exponentials; keys past the tokens are 0, as the softmax sets them.
@@ -324,24 +348,25 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
             p[kt][run][1] = pack_bf16(x[kt][4 * run + 2] * inverse, x[kt][4 * run + 3] * inverse);
         }
     }
-    // A fragment of k-block 2 kt + s: keys kt * 32 + 16 s + 8 half + 0..7,
-    // runs 2 s + half's two halves: the lane's own half and its partner's.
+    // A fragment of k-block 2 kt + s: keys kt * 32 + 16 s + 8 half + 0..7.
+    // Half 0 needs its own run 2 s and its partner's; half 1 its partner's
+    // run 2 s + 1 and its own. v_permlane32_swap of (run 2 s, run 2 s + 1)
+    // trades the upper lanes of the first with the lower lanes of the second
+    // (new first[32 + i] = second[i], new second[i] = first[32 + i]), which
+    // leaves exactly that in (first, second) in every lane.
     Vec16 fragment[2 * KT];
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            const std::uint32_t send0 = half ? p[kt][2 * s][0] : p[kt][2 * s + 1][0];
-            const std::uint32_t send1 = half ? p[kt][2 * s][1] : p[kt][2 * s + 1][1];
-            const std::uint32_t own0 = half ? p[kt][2 * s + 1][0] : p[kt][2 * s][0];
-            const std::uint32_t own1 = half ? p[kt][2 * s + 1][1] : p[kt][2 * s][1];
-            const std::uint32_t got0 = exchange(send0);
-            const std::uint32_t got1 = exchange(send1);
             Vec16& f = fragment[2 * kt + s];
-            f.w[0] = half ? got0 : own0;
-            f.w[1] = half ? got1 : own1;
-            f.w[2] = half ? own0 : got0;
-            f.w[3] = half ? own1 : got1;
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                const auto swapped = __builtin_amdgcn_permlane32_swap(p[kt][2 * s][w], p[kt][2 * s + 1][w],
+                                                                     false, false);
+                f.w[w] = swapped[0];
+                f.w[2 + w] = swapped[1];
+            }
         }
     }
 
@@ -352,16 +377,15 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
     // chains); each keeps the k-block order above.
     Acc acc2[2];
 #pragma unroll
-    for (int d = 0; d < 2; ++d)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            acc2[d][i] = 0.F;
-        }
-#pragma unroll
     for (int kb = 0; kb < kBlocks; ++kb) {
 #pragma unroll
         for (int d = 0; d < 2; ++d) {
-            if (kb < 2 * KT) {
+            if (kb == 0) {
+                const Vec16 v = value_fragment(values, kb, d * kEdge, lane);
+                acc2[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(gemm::bf16x8, v),
+                                                                 __builtin_bit_cast(gemm::bf16x8, fragment[0]),
+                                                                 Acc{}, 0, 0, 0);
+            } else if (kb < 2 * KT) {
                 const Vec16 v = value_fragment(values, kb, d * kEdge, lane);
                 Bf16Mma::run(acc2[d], v, fragment[kb]);
             } else {
@@ -395,6 +419,11 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
     __syncthreads();
     buffer ^= 1;
     pair = next;
+    static_assert(kHeadDim / kKBlock == 4, "four Q fragments");
+    q[0] = q_ahead[0];
+    q[1] = q_ahead[1];
+    q[2] = q_ahead[2];
+    q[3] = q_ahead[3];
     }
 }
 
