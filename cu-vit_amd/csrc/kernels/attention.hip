@@ -29,6 +29,7 @@
 // that (image, head) sit in LDS as [key][head_dim + 4] fp32 (padded rows give
 // conflict-free 16-byte fragment reads).
 #include "device_common.hpp"
+#include "gemm_kernel.hpp"
 #include "launch.hpp"
 
 #include <cmath>
@@ -49,14 +50,13 @@ __device__ __forceinline__ float shuffle_xor(float value, int mask) {
     return __shfl_xor(value, mask, kWave);
 }
 
-template <int Waves>
+template <int KT, int Waves>
 __global__ __launch_bounds__(Waves * kWave) void attention_kernel(const float* __restrict__ qkv,
                                                                   float* __restrict__ context,
                                                                   int heads, int tokens, float scale) {
     extern __shared__ Vec16 lds_vectors[];
     float* const keys = reinterpret_cast<float*>(lds_vectors);
-    const int key_tiles = (tokens + 15) / 16;
-    float* const values = keys + key_tiles * 16 * kPitch;
+    float* const values = keys + KT * 16 * kPitch;
 
     const int t = threadIdx.x;
     const int lane = lane_id();
@@ -70,68 +70,83 @@ __global__ __launch_bounds__(Waves * kWave) void attention_kernel(const float* _
     const int embed = heads * kHeadDim;
     const std::int64_t qkv_row = 3 * static_cast<std::int64_t>(embed);
     const float* const q_base = qkv + static_cast<std::int64_t>(image) * tokens * qkv_row + head * kHeadDim;
-    const float* const k_base = q_base + embed;
-    const float* const v_base = q_base + 2 * embed;
-
-    // K and V of this (image, head) into LDS; rows past the tokens are zero.
-    constexpr int kQuadsPerRow = kHeadDim / 4;
-    for (int q = t; q < key_tiles * 16 * kQuadsPerRow; q += Waves * kWave) {
-        const int row = q / kQuadsPerRow;
-        const int quad = q - row * kQuadsPerRow;
-        float4 k4 = make_float4(0.F, 0.F, 0.F, 0.F);
-        float4 v4 = k4;
-        if (row < tokens) {
-            k4 = *reinterpret_cast<const float4*>(k_base + row * qkv_row + 4 * quad);
-            v4 = *reinterpret_cast<const float4*>(v_base + row * qkv_row + 4 * quad);
-        }
-        *reinterpret_cast<float4*>(keys + row * kPitch + 4 * quad) = k4;
-        *reinterpret_cast<float4*>(values + row * kPitch + 4 * quad) = v4;
-    }
-    __syncthreads();
+    const float* const k_base = q_base + embed; // V follows K by embed in every token's row
 
     const int query_tile = blockIdx.x * Waves + wave;
     const int q0 = query_tile * 16;
-    if (q0 >= tokens) {
-        return; // no barrier follows
-    }
+    const bool live = q0 < tokens; // wavefronts past the tokens still stage K and V
 
     // Q fragments: row q0 + l % 16 (clamped), head_dim chunk 4 (l / 16) of
-    // each k-block.
+    // each k-block, loaded first so that their latency overlaps K's and V's.
     const int q_row = q0 + row_in_tile < tokens ? q0 + row_in_tile : tokens - 1;
+    const auto q_resource = gemm::buffer_resource(q_base);
     Vec16 qf[kHeadDim / 16];
 #pragma unroll
     for (int kb = 0; kb < kHeadDim / 16; ++kb) {
-        qf[kb] = load16(q_base + q_row * qkv_row + 16 * kb + 4 * group);
+        qf[kb] = gemm::buffer_load16(q_resource, static_cast<unsigned int>((q_row * qkv_row + 16 * kb + 4 * group) * 4));
     }
 
-    // Logits: lane holds row q0 + l % 16, keys 16 jt + 4 (l / 16) + r.
-    floatx4 s[kMaxKeyTiles];
+    // K and V of this (image, head), all loads in flight at once (rows past
+    // the tokens read as zero). K goes to LDS first; V's stores wait until
+    // the logits and the softmax are done, so V's loads land meanwhile.
+    constexpr int kQuadsPerRow = kHeadDim / 4;
+    constexpr int kQuads = KT * 16 * kQuadsPerRow;
+    constexpr int kPerThread = (kQuads + Waves * kWave - 1) / (Waves * kWave);
+    const auto kv_resource = gemm::buffer_resource(k_base);
+    Vec16 kreg[kPerThread];
+    Vec16 vreg[kPerThread];
 #pragma unroll
-    for (int jt = 0; jt < kMaxKeyTiles; ++jt) {
-        s[jt] = floatx4{0.F, 0.F, 0.F, 0.F};
-        if (jt < key_tiles) {
+    for (int i = 0; i < kPerThread; ++i) {
+        const int q = t + i * Waves * kWave;
+        const int row = q / kQuadsPerRow;
+        const bool inside = q < kQuads && row < tokens;
+        const unsigned int offset = static_cast<unsigned int>((row * qkv_row + 4 * (q % kQuadsPerRow)) * 4);
+        kreg[i] = gemm::buffer_load16(kv_resource, inside ? offset : gemm::kOutside);
+        vreg[i] = gemm::buffer_load16(kv_resource, inside ? offset + 4U * embed : gemm::kOutside);
+    }
+    auto stage = [&](float* tile, const Vec16 (&reg)[kPerThread]) {
 #pragma unroll
-            for (int kb = 0; kb < kHeadDim / 16; ++kb) {
-                const Vec16 kf = load16(keys + (16 * jt + row_in_tile) * kPitch + 16 * kb + 4 * group);
+        for (int i = 0; i < kPerThread; ++i) {
+            const int q = t + i * Waves * kWave;
+            if (kQuads % (Waves * kWave) == 0 || q < kQuads) {
+                store16(tile + (q / kQuadsPerRow) * kPitch + 4 * (q % kQuadsPerRow), reg[i]);
+            }
+        }
+    };
+    stage(keys, kreg);
+    __syncthreads();
+
+    // Logits: lane holds row q0 + l % 16, keys 16 jt + 4 (l / 16) + r. The
+    // first MFMA of a tile takes its zero accumulator as a constant.
+    floatx4 s[KT];
+    if (live) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    s[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(kf.w[e]),
-                                                                 __uint_as_float(qf[kb].w[e]), s[jt],
-                                                                 0, 0, 0);
-                }
+    for (int jt = 0; jt < KT; ++jt) {
+#pragma unroll
+        for (int kb = 0; kb < kHeadDim / 16; ++kb) {
+            const Vec16 kf = load16(keys + (16 * jt + row_in_tile) * kPitch + 16 * kb + 4 * group);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                s[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(kf.w[e]),
+                                                             __uint_as_float(qf[kb].w[e]),
+                                                             kb == 0 && e == 0 ? floatx4{0.F, 0.F, 0.F, 0.F} : s[jt],
+                                                             0, 0, 0);
             }
         }
     }
 
-    // Row max over the valid keys (exact in any order).
+    // alpha * sum, rounded on its own as the GEMM epilogue stores it (never
+    // fused into the subtraction below), then the row max over the valid
+    // keys (exact in any order); only the last key tile holds keys past the
+    // tokens.
     float maximum = -INFINITY;
 #pragma unroll
-    for (int jt = 0; jt < kMaxKeyTiles; ++jt) {
+    for (int jt = 0; jt < KT; ++jt) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int key = 16 * jt + 4 * group + r;
+#pragma clang fp contract(off)
             s[jt][r] = scale * s[jt][r];
-            if (key < tokens) {
+            if (jt < KT - 1 || 16 * jt + 4 * group + r < tokens) {
                 maximum = fmaxf(maximum, s[jt][r]);
             }
         }
@@ -141,11 +156,11 @@ __global__ __launch_bounds__(Waves * kWave) void attention_kernel(const float* _
 
     // Exponentials; keys past the tokens become exact zeros.
 #pragma unroll
-    for (int jt = 0; jt < kMaxKeyTiles; ++jt) {
+    for (int jt = 0; jt < KT; ++jt) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int key = 16 * jt + 4 * group + r;
-            s[jt][r] = key < tokens ? __builtin_amdgcn_exp2f((s[jt][r] - maximum) * kLog2e) : 0.F;
+            const float e = __builtin_amdgcn_exp2f((s[jt][r] - maximum) * kLog2e);
+            s[jt][r] = jt < KT - 1 || 16 * jt + 4 * group + r < tokens ? e : 0.F;
         }
     }
 
@@ -155,12 +170,13 @@ __global__ __launch_bounds__(Waves * kWave) void attention_kernel(const float* _
     // pairs (t ^ 1), quads (t ^ 2), quad 0 + quad 1 and quad 2 + quad 3 (the
     // half-row mirror), and the two halves (the row mirror); here the quad
     // totals sit in the four lanes of a query row, one exchange per level.
+    // Tiles past the row (up to the softmax kernel's 16) would add +0.
     float partial[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         float sum = 0.F;
 #pragma unroll
-        for (int jt = 0; jt < kMaxKeyTiles; ++jt) {
+        for (int jt = 0; jt < KT; ++jt) {
             sum += s[jt][r];
         }
         partial[r] = sum;
@@ -169,31 +185,34 @@ __global__ __launch_bounds__(Waves * kWave) void attention_kernel(const float* _
     const float half = quad + shuffle_xor(quad, 16);
     const float inverse = 1.0F / (half + shuffle_xor(half, 32));
 #pragma unroll
-    for (int jt = 0; jt < kMaxKeyTiles; ++jt) {
+    for (int jt = 0; jt < KT; ++jt) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             s[jt][r] *= inverse;
         }
     }
 
+    } // live
+
+    stage(values, vreg);
+    __syncthreads();
+    if (!live) {
+        return; // no barrier follows
+    }
+
     // weights.V: lane provides weights[row][keys 16 jt + 4 g + e] (its own
     // registers) and V[keys 16 jt + 4 g + e][16 dt + l % 16].
     floatx4 out[kHeadDim / 16];
 #pragma unroll
-    for (int dt = 0; dt < kHeadDim / 16; ++dt) {
-        out[dt] = floatx4{0.F, 0.F, 0.F, 0.F};
-    }
+    for (int jt = 0; jt < KT; ++jt) {
+        const float* const v_rows = values + (16 * jt + 4 * group) * kPitch + row_in_tile;
 #pragma unroll
-    for (int jt = 0; jt < kMaxKeyTiles; ++jt) {
-        if (jt < key_tiles) {
-            const float* const v_rows = values + (16 * jt + 4 * group) * kPitch + row_in_tile;
+        for (int dt = 0; dt < kHeadDim / 16; ++dt) {
 #pragma unroll
-            for (int dt = 0; dt < kHeadDim / 16; ++dt) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    out[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(v_rows[e * kPitch + 16 * dt], s[jt][e],
-                                                                   out[dt], 0, 0, 0);
-                }
+            for (int e = 0; e < 4; ++e) {
+                out[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                    v_rows[e * kPitch + 16 * dt], s[jt][e],
+                    jt == 0 && e == 0 ? floatx4{0.F, 0.F, 0.F, 0.F} : out[dt], 0, 0, 0);
             }
         }
     }
@@ -213,6 +232,23 @@ __global__ __launch_bounds__(Waves * kWave) void attention_kernel(const float* _
 
 constexpr int kWaves = 8;
 
+template <int KT>
+hipError_t launch(const float* qkv, float* context, int images, int heads, int tokens,
+                  hipStream_t stream) {
+    constexpr std::size_t kLds = 2 * static_cast<std::size_t>(KT) * 16 * kPitch * sizeof(float);
+    auto kernel = attention_kernel<KT, kWaves>;
+    static std::atomic<std::uint64_t> opted_in{0};
+    if (const hipError_t opted = allow_lds(reinterpret_cast<const void*>(kernel), kLds, opted_in);
+        opted != hipSuccess) {
+        return opted;
+    }
+    const dim3 grid(static_cast<unsigned int>((KT + kWaves - 1) / kWaves),
+                    static_cast<unsigned int>(images * heads));
+    const float scale = 1.0F / std::sqrt(static_cast<float>(kHeadDim));
+    kernel<<<grid, kWaves * kWave, kLds, stream>>>(qkv, context, heads, tokens, scale);
+    return hipGetLastError();
+}
+
 } // namespace
 
 bool attention_supported(int tokens, int head_dim) {
@@ -224,20 +260,26 @@ hipError_t attention_f32(const float* qkv, float* context, int images, int heads
     if (!attention_supported(tokens, head_dim)) {
         return hipErrorInvalidValue;
     }
-    const int key_tiles = (tokens + 15) / 16;
-    const std::size_t lds = 2 * static_cast<std::size_t>(key_tiles) * 16 * kPitch * sizeof(float);
-    static std::atomic<std::uint64_t> opted_in{0};
-    if (const hipError_t opted =
-            allow_lds(reinterpret_cast<const void*>(attention_kernel<kWaves>),
-                      2 * 16 * kMaxKeyTiles * kPitch * sizeof(float), opted_in);
-        opted != hipSuccess) {
-        return opted;
+    // One instance per key-tile count: the tiles are compile-time, and only
+    // the last one carries keys past the tokens.
+    switch ((tokens + 15) / 16) {
+    case 1: return launch<1>(qkv, context, images, heads, tokens, stream);
+    case 2: return launch<2>(qkv, context, images, heads, tokens, stream);
+    case 3: return launch<3>(qkv, context, images, heads, tokens, stream);
+    case 4: return launch<4>(qkv, context, images, heads, tokens, stream);
+    case 5: return launch<5>(qkv, context, images, heads, tokens, stream);
+    case 6: return launch<6>(qkv, context, images, heads, tokens, stream);
+    case 7: return launch<7>(qkv, context, images, heads, tokens, stream);
+    case 8: return launch<8>(qkv, context, images, heads, tokens, stream);
+    case 9: return launch<9>(qkv, context, images, heads, tokens, stream);
+    case 10: return launch<10>(qkv, context, images, heads, tokens, stream);
+    case 11: return launch<11>(qkv, context, images, heads, tokens, stream);
+    case 12: return launch<12>(qkv, context, images, heads, tokens, stream);
+    case 13: return launch<13>(qkv, context, images, heads, tokens, stream);
+    case 14: return launch<14>(qkv, context, images, heads, tokens, stream);
+    case 15: return launch<15>(qkv, context, images, heads, tokens, stream);
+    default: return launch<kMaxKeyTiles>(qkv, context, images, heads, tokens, stream);
     }
-    const dim3 grid(static_cast<unsigned int>((key_tiles + kWaves - 1) / kWaves),
-                    static_cast<unsigned int>(images * heads));
-    const float scale = 1.0F / std::sqrt(static_cast<float>(head_dim));
-    attention_kernel<kWaves><<<grid, kWaves * kWave, lds, stream>>>(qkv, context, heads, tokens, scale);
-    return hipGetLastError();
 }
 
 } // namespace cuvit::detail
