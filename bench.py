@@ -490,7 +490,8 @@ def vit_base_bf16_counters(torch, cuvit, flush):
     """The ViT-Base batch-64 bf16 kernels for the counter passes, three cold
     launches each: LN [12608, 768], softmax [151296, 197] in place, the patch
     gather [64, 3, 224, 224], FC1 with the GELU epilogue and the fused
-    attention; then the fp32 fused attention at ViT-Tiny batch 32."""
+    attention; then the fp32 fused attention and the fp32 FC1 + GELU GEMM
+    (6304 x 768 x 192) at ViT-Tiny batch 32."""
     rows, embed, hidden, heads, batch = 64 * TOKENS, 768, 3072, 12, 64
     bf = torch.bfloat16
     x = torch.randn(rows * embed, device="cuda").to(bf)
@@ -509,6 +510,13 @@ def vit_base_bf16_counters(torch, cuvit, flush):
     context = torch.empty(rows * embed, device="cuda", dtype=bf)
     tiny_qkv = torch.randn(BATCH * TOKENS * 3 * 192, device="cuda")
     tiny_context = torch.empty(BATCH * TOKENS * 192, device="cuda")
+    tiny_rows = (BATCH * TOKENS, 768, 192)
+    tiny_a = torch.randn(tiny_rows[0] * tiny_rows[2], device="cuda")
+    tiny_w = 0.02 * torch.randn(tiny_rows[1] * tiny_rows[2], device="cuda")
+    tiny_bias = torch.zeros(tiny_rows[1], device="cuda")
+    tiny_c = torch.empty(tiny_rows[0] * tiny_rows[1], device="cuda")
+    tiny_problem = cuvit.gemm_problem(*tiny_rows, cuvit.TRANSPOSED)
+    tiny_problem.epilogue.gelu = 1
     steps = {
         "bf16 layer_norm [12608,768]": lambda: cuvit.layer_norm(x, gamma, beta, y, rows, embed, 1e-6),
         "bf16 softmax [151296,197]": lambda: cuvit.softmax(logits, logits, batch * heads * TOKENS, TOKENS),
@@ -518,6 +526,8 @@ def vit_base_bf16_counters(torch, cuvit, flush):
         "bf16 attention ViT-Base b64": lambda: cuvit.attention(qkv, context, batch, heads, TOKENS, 64),
         "fp32 attention ViT-Tiny b32": lambda: cuvit.attention(tiny_qkv, tiny_context, BATCH, 3,
                                                                TOKENS, 64),
+        "fp32 fc1_gelu_gemm 6304x768x192": lambda: cuvit.gemm(tiny_a, tiny_w, tiny_bias, tiny_c,
+                                                              tiny_problem),
     }
     for name, launch in steps.items():
         for i in range(3):
