@@ -61,6 +61,21 @@ def test_fused_attention_is_bitwise_the_launch_sequence(cuvit, oracle, device, i
                   f"fused attention {images}x{heads}x{tokens} differs from the launch sequence")
 
 
+@pytest.mark.parametrize("key_tiles", range(1, 17))
+def test_every_key_tile_count_is_bitwise_the_launch_sequence(cuvit, oracle, device, key_tiles):
+    """The fp32 kernel is one instance per count of 16-key tiles: each, with
+    a full last tile and with one holding 9 keys."""
+    images, heads = 2, 2
+    embed = heads * HEAD_DIM
+    for tokens in (16 * key_tiles, 16 * key_tiles - 7):
+        qkv = to_device(oracle.generator(7200 + tokens).normal(images * tokens * 3 * embed), device)
+        expected = unfused(cuvit, qkv, images, heads, tokens, device)
+        context = torch.full((images * tokens * embed,), float("nan"), device=device)
+        cuvit.attention(qkv, context, images, heads, tokens, HEAD_DIM)
+        require_exact(to_host(context), to_host(expected),
+                      f"fused attention {images}x{heads}x{tokens} differs from the launch sequence")
+
+
 def test_fused_attention_matches_the_oracle(cuvit, oracle, device):
     images, heads, tokens = 2, 3, 37
     embed = heads * HEAD_DIM
