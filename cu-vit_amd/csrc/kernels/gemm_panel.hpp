@@ -12,16 +12,16 @@
 //
 // Same arithmetic as gemm_kernel<float>: lane l holds row l % 16 of A and of
 // the panel at k chunk l / 16, k-blocks of 16 are walked in ascending order
-// over K (a multiple of 64 here, as the tiled kernel rounds it), and element s
-// of a fragment feeds the
-// s-th of four v_mfma_f32_16x16x4_f32 (B fragment as the first operand). So
-// every accumulator sees the same MFMAs with the same operands in the same
-// order as in the LDS-tiled kernel, and the two give bitwise equal results;
-// the epilogue (alpha, bias, GELU, store or accumulate) is the same function.
-// Rows past M and panel rows past N read as zero; results past M are not
-// stored, and N is a multiple of 4 so a run of four columns is all in or all
-// out. An out-of-range offset past kOutside plus a group's 64-byte steps
-// stays past the buffer resource's record count, so it reads zero.
+// over K (here a multiple of 64, as the tiled kernel rounds it), and element
+// s of a fragment feeds the s-th of four v_mfma_f32_16x16x4_f32 (B fragment
+// as the first operand). So every accumulator sees the same MFMAs with the
+// same operands in the same order as in the LDS-tiled kernel, and the two
+// give bitwise equal results; the epilogue (alpha, bias, GELU, store or
+// accumulate) takes the same steps. Rows past M and panel rows past N read
+// as zero; results past M are not stored, and N is a multiple of 4 so a run
+// of four columns is all in or all out. An out-of-range offset (kOutside)
+// plus a group's 64-byte steps stays past the buffer resource's record
+// count, so it reads zero.
 #pragma once
 
 #include "gemm_kernel.hpp"
@@ -64,7 +64,9 @@ template <int KB, int BN, int TN, int KG, int W> struct PanelShape {
 /// the rest are cut into half items (16 x 8 TN) dealt the same way, so no
 /// SIMD carries more than half an item beyond another: the MFMA pipe is the
 /// bound, and a whole item's difference would idle three SIMDs for its
-/// length. The wavefronts of a SIMD take its items in turn.
+/// length. The wavefronts of a SIMD take its items in turn; wavefronts w and
+/// w + 4 share a SIMD (the CU places a workgroup's wavefronts on its SIMDs
+/// in turn, read from the hardware id register on MI355X).
 template <int KB, int BN, int TN, int KG, int W, bool kAlpha, bool kBias, bool kGelu, bool kAccumulate>
 __global__ __launch_bounds__(kWave * W) void gemm_panel_kernel(const float* __restrict__ a,
                                                              const float* __restrict__ b,
