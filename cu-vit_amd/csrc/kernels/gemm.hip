@@ -103,7 +103,7 @@ hipError_t launch(const T* a, const T* b, const float* bias, T* c, const GemmArg
     }
     const dim3 grid(static_cast<unsigned int>(tiles),
                     static_cast<unsigned int>(args.count < kMaxGridY ? args.count : kMaxGridY));
-    kernel<<<grid, kThreads, S::kLdsBytes, stream>>>(a, b, bias, c, args, map, vector_c);
+    kernel<<<grid, S::kThreads, S::kLdsBytes, stream>>>(a, b, bias, c, args, map, vector_c);
     return hipGetLastError();
 }
 
@@ -291,7 +291,25 @@ hipError_t gemm_bf16(const std::uint16_t* a, const std::uint16_t* b, const float
         wide != hipErrorNotSupported) {
         return wide;
     }
-    if (tile_count(args, 128, 128) >= static_cast<std::int64_t>(compute_units()) * 2) {
+    // One round of 256 x 192 tiles, eight wavefronts of 64 x 96, for long
+    // products with B as [N, K] that would need more than two 128 x 128 tiles
+    // per CU: each CU then streams one tile's whole K (ViT-Base FC2 12608 x
+    // 768 x 3072, accumulating: 110 -> 92 us). Shorter K keeps the tiles
+    // below (the projection, K = 768: 44 against 49 us).
+    const std::int64_t units = compute_units();
+    if (args.transposed && args.k >= 2048 && tile_count(args, 256, 192) <= units &&
+        tile_count(args, 128, 128) > 2 * units) {
+        using S = Shape<std::uint16_t, 4, 2, 2, 3, 64>;
+        const bool split = args.inner > 0;
+        if (vector_operand(a, args.lda, args.k, args.stride_a, args.outer_stride_a, split) &&
+            vector_operand(b, args.ldb, args.k, args.stride_b, args.outer_stride_b, split) &&
+            static_cast<std::int64_t>(S::kBM) * args.lda * 2 < gemm::kMaxSpan &&
+            static_cast<std::int64_t>(S::kBN) * args.ldb * 2 < gemm::kMaxSpan) {
+            return launch<std::uint16_t, 4, 2, 2, 3, 64, 2, true, true, true>(
+                a, b, bias, c, args, vector_output(c, args), stream);
+        }
+    }
+    if (tile_count(args, 128, 128) >= units * 2) {
         // Up to K = 1024, 32-deep stages with registers for three workgroups
         // per CU beat 64-deep ones at two (ViT-Base FC1 + GELU 146 -> 136 us,
         // QKV 103 -> 96, projection 45.5 -> 38.4); FC2 (K = 3072) keeps the

@@ -9,14 +9,16 @@
 // (entry * stride) or split into (entry / inner, entry % inner) with outer
 // strides (gemm.cu:58-72); every operand has its own leading dimension.
 //
-// Structure. A workgroup of four wavefronts owns a BM x BN tile of C; each
+// Structure. A workgroup of WM x WN wavefronts (four, or eight for the
+// largest bf16 tiles) owns a BM x BN tile of C; each
 // wavefront owns (TM * E) x (TN * E) of it as TM x TN MFMA tiles of edge E.
 // K is walked in BK-wide stages. Both operand tiles sit in LDS as
 // [rows][BK] (k contiguous), rows padded by 16 bytes so that the sixteen
 // lanes reading one fragment column hit sixteen different bank quads. Stages
 // are double-buffered in LDS and fetched from global memory into registers
 // two stages ahead, so a global load has two stages of MFMA work to land and
-// each stage costs one barrier.
+// each stage costs one barrier (one stage ahead for eight wavefronts with
+// 64-deep stages, whose registers hold one stage's fetch, not two).
 //
 // MFMA. fp32 uses v_mfma_f32_16x16x4_f32 (E = 16) and bf16
 // v_mfma_f32_32x32x16_bf16 (E = 32); measured on MI355X with an in-kernel
@@ -55,6 +57,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+/// Threads of a four-wavefront workgroup (the wide and tiled bf16 kernels).
 constexpr int kThreads = 256;
 
 /// The MFMA of each storage type. kEdge is the MFMA tile's edge; a lane's
@@ -230,7 +233,8 @@ __device__ __forceinline__ void store4(std::uint16_t* p, const float (&value)[4]
 
 /// Compile-time shape of one kernel instance.
 template <typename T, int WM, int WN, int TM, int TN, int BK> struct Shape {
-    static_assert(WM * WN == 4, "four wavefronts per workgroup");
+    static_assert(WM * WN == 4 || WM * WN == 8, "four or eight wavefronts per workgroup");
+    static constexpr int kThreads = kWave * WM * WN;
     static constexpr int kE = Mma<T>::kEdge;
     static constexpr int kBM = WM * TM * kE;
     static constexpr int kBN = WN * TN * kE;
@@ -292,7 +296,7 @@ template <typename T> constexpr int kSpan = sizeof(T) == 2 ? 128 : 64;
 /// (amdgpu_waves_per_eu); 1 leaves the compiler free.
 template <typename T, int WM, int WN, int TM, int TN, int BK, bool VecA, bool VecB, bool TransB,
           int MinWaves>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(MinWaves))) void gemm_kernel(const T* __restrict__ a,
+__global__ __launch_bounds__(kWave * WM * WN) __attribute__((amdgpu_waves_per_eu(MinWaves))) void gemm_kernel(const T* __restrict__ a,
                                                         const T* __restrict__ b,
                                                         const float* __restrict__ bias, T* c,
                                                         GemmArgs args, TileMap map, bool vector_c) {
@@ -371,8 +375,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(MinWav
             const int k0 = step * BK;
 #pragma unroll
             for (int p = 0; p < S::kAPerThread; ++p) {
-                const int q = t + kThreads * p;
-                if (S::kAChunks % kThreads == 0 || q < S::kAChunks) {
+                const int q = t + S::kThreads * p;
+                if (S::kAChunks % S::kThreads == 0 || q < S::kAChunks) {
                     const int row = q / S::kChunksPerRow;
                     const int k = k0 + V * (q % S::kChunksPerRow);
                     if constexpr (VecA) {
@@ -385,8 +389,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(MinWav
             }
 #pragma unroll
             for (int p = 0; p < S::kBPerThread; ++p) {
-                const int q = t + kThreads * p;
-                if (S::kBChunks % kThreads == 0 || q < S::kBChunks) {
+                const int q = t + S::kThreads * p;
+                if (S::kBChunks % S::kThreads == 0 || q < S::kBChunks) {
                     if constexpr (TransB) {
                         const int row = q / S::kChunksPerRow;
                         const int k = k0 + V * (q % S::kChunksPerRow);
@@ -419,16 +423,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(MinWav
             T* const tile_b = tile_a + BM * P;
 #pragma unroll
             for (int p = 0; p < S::kAPerThread; ++p) {
-                const int q = t + kThreads * p;
-                if (S::kAChunks % kThreads == 0 || q < S::kAChunks) {
+                const int q = t + S::kThreads * p;
+                if (S::kAChunks % S::kThreads == 0 || q < S::kAChunks) {
                     const int row = q / S::kChunksPerRow;
                     store16(tile_a + row * P + V * S::place(row, q % S::kChunksPerRow), ra[p]);
                 }
             }
 #pragma unroll
             for (int p = 0; p < S::kBPerThread; ++p) {
-                const int q = t + kThreads * p;
-                if (S::kBChunks % kThreads == 0 || q < S::kBChunks) {
+                const int q = t + S::kThreads * p;
+                if (S::kBChunks % S::kThreads == 0 || q < S::kBChunks) {
                     if constexpr (TransB) {
                         const int row = q / S::kChunksPerRow;
                         store16(tile_b + row * P + V * S::place(row, q % S::kChunksPerRow), rb[p]);
@@ -525,7 +529,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(MinWav
         // that started at +0, which changes no bit of them. So every path
         // through the loop has the same loads in flight, each LDS write waits
         // only for its own set, and the accumulators stay in place.
-        if (steps > 0) {
+        // Eight wavefronts of 64-deep stages run with one register set: at two
+        // wavefronts per SIMD a lane has 256 registers, and a second set of
+        // the stage's fetch (28 of them) spills. A stage's loads are then
+        // issued during the stage before it and written to LDS at its end.
+        constexpr bool kOneSet = S::kThreads == 512 && BK == 64;
+        if (kOneSet && steps > 0) {
+            fetch(ra0, rb0, 0);
+            stage(ra0, rb0, 0);
+            fetch(ra0, rb0, 1);
+            __syncthreads();
+            for (int step = 0; step < steps; step += 2) {
+                advance(ra0, rb0, ra0, rb0, 0, step + 2);
+                __syncthreads();
+                advance(ra0, rb0, ra0, rb0, 1, step + 3);
+                __syncthreads();
+            }
+        } else if (steps > 0) {
             fetch(ra0, rb0, 0);
             stage(ra0, rb0, 0);
             fetch(ra1, rb1, 1);
