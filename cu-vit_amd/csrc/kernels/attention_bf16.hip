@@ -11,7 +11,9 @@
 //   * logits: the GEMM's v_mfma_f32_32x32x16_bf16 over head_dim in k-blocks
 //     of 16 with the same operand roles (K fragment first, Q fragment
 //     second; lane l reads row l % 32 and k chunk 8 (l / 32)), then
-//     alpha * sum rounded to bf16, as the GEMM epilogue stores it;
+//     alpha * sum rounded to bf16, as the GEMM epilogue stores it (alpha =
+//     1/8 enters as a factor of the exponential's constant, which gives
+//     the same bits);
 //   * softmax: the bf16 row softmax's own code (softmax_terms.hpp, teams of
 //     16 lanes, column c on team lane c % 16) over the bf16 logits, each
 //     probability rounded to bf16;
@@ -72,6 +74,10 @@ constexpr int kMaxTokens = 256;
 constexpr int kMaxKeyTiles = kMaxTokens / kEdge;
 constexpr int kMaxWaves = 8;
 constexpr int kWavesPerGroup = 4;
+/// log2 e / sqrt(head_dim): the logits' scale, 1/8 (a power of two), folded
+/// into the exponential's base-2 constant.
+constexpr float kScaledLog2e = kLog2e * 0.125F;
+static_assert(kHeadDim == 64, "the logits' scale is 1/8");
 
 /// Elements per LDS row of K ([key][head_dim + 8]).
 constexpr int kKeyPitch = kHeadDim + 8;
@@ -159,7 +165,7 @@ __device__ __forceinline__ PairBases pair_bases(const std::uint16_t* qkv, int pa
 template <int KT, int Chunks>
 __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
     const std::uint16_t* __restrict__ qkv, std::uint16_t* __restrict__ context, int heads,
-    int tokens, int pairs, float scale) {
+    int tokens, int pairs) {
     constexpr int kPadded = KT * kEdge;
     constexpr int kBufferElements = kPadded * (kHeadDim + kKeyPitch);
     extern __shared__ Vec16 lds_vectors[];
@@ -277,17 +283,24 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
         }
     }
 
-    // alpha * sum rounded to bf16, two logits per conversion (the same
-    // rounding as one at a time). The row max over the valid keys is exact
-    // in any order, and rounding to nearest never reverses an order, so the
-    // max of the rounded logits is the rounded max of the unrounded ones:
-    // it is taken over the products, which need no canonicalizing.
+    // The GEMM stores alpha * sum rounded to bf16, alpha = 1/8. A power of
+    // two commutes with rounding to nearest (bf16 or float), with the max and
+    // with a difference of two such values, and log2 e / 8 is as exact as
+    // log2 e: the softmax's exponent (round(sum / 8) - round(max / 8)) * log2 e
+    // is (round(sum) - round(max)) * (log2 e / 8), bit for bit, whenever the
+    // scaled values are normal floats. (Below 2^-126 the two differ only by
+    // less than an exponent of 2^-120, which exp2 returns as 1 either way.)
+    // So the sums are rounded unscaled, two per conversion (the same rounding
+    // as one at a time), and the 1/8 rides in the exponent's constant. The
+    // row max over the valid keys is exact in any order, and rounding to
+    // nearest never reverses an order, so the max of the rounded logits is
+    // the rounded max of the unrounded ones: it is taken over the products,
+    // which need no canonicalizing.
     float maximum = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            x[kt][i] = scale * x[kt][i];
             const int key = kt * kEdge + Bf16Mma::column(lane, i / 4) + i % 4;
             // Only the last key tile holds keys past the tokens.
             if (kt < KT - 1 || key < tokens) {
@@ -310,7 +323,9 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int key = kt * kEdge + Bf16Mma::column(lane, i / 4) + i % 4;
-            x[kt][i] = kt < KT - 1 || key < tokens ? shifted_exp(x[kt][i], maximum) : 0.F;
+            x[kt][i] = kt < KT - 1 || key < tokens
+                           ? __builtin_amdgcn_exp2f((x[kt][i] - maximum) * kScaledLog2e)
+                           : 0.F;
         }
     }
 
@@ -439,7 +454,6 @@ hipError_t launch(const std::uint16_t* qkv, std::uint16_t* context, int images, 
     const bool many = pairs >= 2 * static_cast<std::int64_t>(compute_units());
     const int per_group = many ? kMaxWaves : kWavesPerGroup;
     const int waves = query_tiles < per_group ? query_tiles : per_group;
-    const float scale = 1.0F / std::sqrt(static_cast<float>(kHeadDim));
     // (Up to 7 key tiles, 224 tokens: with 8 the prefetch registers spill.)
     if constexpr (KT <= 7) {
     if (many && pairs <= 0x7FFFFFFF) {
@@ -458,7 +472,7 @@ hipError_t launch(const std::uint16_t* qkv, std::uint16_t* context, int images, 
         }
         const std::int64_t groups = compute_units() < pairs ? compute_units() : pairs;
         kernel<<<dim3(1, static_cast<unsigned int>(groups)), query_tiles * kWave, 2 * lds_bytes(KT),
-                 stream>>>(qkv, context, heads, tokens, static_cast<int>(pairs), scale);
+                 stream>>>(qkv, context, heads, tokens, static_cast<int>(pairs));
         return hipGetLastError();
     }
     }
@@ -473,7 +487,7 @@ hipError_t launch(const std::uint16_t* qkv, std::uint16_t* context, int images, 
     const dim3 grid(static_cast<unsigned int>((query_tiles + waves - 1) / waves),
                     static_cast<unsigned int>(pairs));
     kernel<<<grid, waves * kWave, lds_bytes(KT), stream>>>(qkv, context, heads, tokens,
-                                                          static_cast<int>(pairs), scale);
+                                                          static_cast<int>(pairs));
     return hipGetLastError();
 }
 

@@ -166,6 +166,25 @@ def test_fused_attention_bf16_is_bitwise_the_launch_sequence(cuvit, oracle, devi
                   f"bf16 fused attention {images}x{heads}x{tokens} differs from the launch sequence")
 
 
+@pytest.mark.parametrize("stddev", [1.1e-19, 1.0e-10, 30.0])
+def test_fused_attention_bf16_extreme_logits_are_bitwise_the_launch_sequence(cuvit, oracle, device,
+                                                                            stddev):
+    """Logits whose scaled values straddle the smallest normal float (inputs
+    of about 1e-19: the GEMM rounds sum / 8, the fused kernel folds the 1/8
+    into its exponential), tiny normal ones, and large ones whose
+    exponentials underflow: the same bits as the three launches."""
+    from conftest import bf16_bits
+
+    images, heads, tokens = 2, 3, 197
+    embed = heads * HEAD_DIM
+    qkv = bf16_qkv(oracle, 7500, images * tokens * 3 * embed, device, stddev)
+    expected = unfused_bf16(cuvit, qkv, images, heads, tokens, device)
+    context = torch.full((images * tokens * embed,), float("nan"), device=device, dtype=torch.bfloat16)
+    cuvit.attention(qkv, context, images, heads, tokens, HEAD_DIM)
+    require_exact(bf16_bits(context), bf16_bits(expected),
+                  f"bf16 fused attention with inputs of scale {stddev} differs from the launch sequence")
+
+
 def test_fused_attention_bf16_rounds_like_the_oracle(cuvit, oracle, device):
     """Against the oracle's fp32 attention with the bf16 rounding points
     (logits and probabilities rounded as the model stores them): equal bits
