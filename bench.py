@@ -489,9 +489,10 @@ def counters(torch, cuvit, pools):
 def vit_base_bf16_counters(torch, cuvit, flush):
     """The ViT-Base batch-64 bf16 kernels for the counter passes, three cold
     launches each: LN [12608, 768], softmax [151296, 197] in place, the patch
-    gather [64, 3, 224, 224], FC1 with the GELU epilogue and the fused
-    attention; then the fp32 fused attention and the fp32 FC1 + GELU GEMM
-    (6304 x 768 x 192) at ViT-Tiny batch 32."""
+    gather [64, 3, 224, 224], FC1 with the GELU epilogue, FC2 accumulating
+    into the residual stream (12608 x 768 x 3072) and the fused attention;
+    then the fp32 fused attention and the fp32 FC1 + GELU GEMM (6304 x 768 x
+    192) at ViT-Tiny batch 32."""
     rows, embed, hidden, heads, batch = 64 * TOKENS, 768, 3072, 12, 64
     bf = torch.bfloat16
     x = torch.randn(rows * embed, device="cuda").to(bf)
@@ -506,6 +507,10 @@ def vit_base_bf16_counters(torch, cuvit, flush):
     c = torch.empty(rows * hidden, device="cuda", dtype=bf)
     problem = cuvit.gemm_problem(rows, hidden, embed, cuvit.TRANSPOSED)
     problem.epilogue.gelu = 1
+    # FC2 reads the [rows, hidden] activations and W2 as [embed, hidden] (W1's
+    # storage, the same element count) and adds into the residual stream y.
+    fc2_problem = cuvit.gemm_problem(rows, embed, hidden, cuvit.TRANSPOSED)
+    fc2_problem.epilogue.accumulate = 1
     qkv = torch.randn(rows * 3 * embed, device="cuda").to(bf)
     context = torch.empty(rows * embed, device="cuda", dtype=bf)
     tiny_qkv = torch.randn(BATCH * TOKENS * 3 * 192, device="cuda")
@@ -523,6 +528,7 @@ def vit_base_bf16_counters(torch, cuvit, flush):
         "bf16 extract_patches b64": lambda: cuvit.extract_patches(images, patches, batch, CHANNELS,
                                                                   IMAGE, IMAGE, PATCH),
         "bf16 fc1_gelu_gemm 12608x3072x768": lambda: cuvit.gemm(x, w, bias, c, problem),
+        "bf16 fc2_gemm 12608x768x3072 accumulating": lambda: cuvit.gemm(c, w, bias, y, fc2_problem),
         "bf16 attention ViT-Base b64": lambda: cuvit.attention(qkv, context, batch, heads, TOKENS, 64),
         "fp32 attention ViT-Tiny b32": lambda: cuvit.attention(tiny_qkv, tiny_context, BATCH, 3,
                                                                TOKENS, 64),

@@ -291,21 +291,23 @@ hipError_t gemm_bf16(const std::uint16_t* a, const std::uint16_t* b, const float
         wide != hipErrorNotSupported) {
         return wide;
     }
-    // One round of 256 x 192 tiles, eight wavefronts of 64 x 96, for long
-    // products with B as [N, K] that would need more than two 128 x 128 tiles
-    // per CU: each CU then streams one tile's whole K (ViT-Base FC2 12608 x
-    // 768 x 3072, accumulating: 110 -> 92 us). Shorter K keeps the tiles
-    // below (the projection, K = 768: 44 against 49 us).
+    // One round of 256 x 192 tiles, twelve wavefronts of 64 x 64 (three per
+    // SIMD), for products with B as [N, K] that would need more than two
+    // 128 x 128 tiles per CU: each CU then streams one tile's whole K, with
+    // three wavefronts per SIMD to cover the loads (ViT-Base FC2 12608 x 768 x
+    // 3072, accumulating: 110 -> 81 us; the projection, K = 768: 43 -> 40 us).
+    // Eight wavefronts of 64 x 96 ran FC2 in 92-95 us and the projection in
+    // 49: two per SIMD left the waves waiting on their loads 54% of the time.
     const std::int64_t units = compute_units();
-    if (args.transposed && args.k >= 2048 && tile_count(args, 256, 192) <= units &&
+    if (args.transposed && args.k >= 512 && tile_count(args, 256, 192) <= units &&
         tile_count(args, 128, 128) > 2 * units) {
-        using S = Shape<std::uint16_t, 4, 2, 2, 3, 64>;
+        using S = Shape<std::uint16_t, 4, 3, 2, 2, 64>;
         const bool split = args.inner > 0;
         if (vector_operand(a, args.lda, args.k, args.stride_a, args.outer_stride_a, split) &&
             vector_operand(b, args.ldb, args.k, args.stride_b, args.outer_stride_b, split) &&
             static_cast<std::int64_t>(S::kBM) * args.lda * 2 < gemm::kMaxSpan &&
             static_cast<std::int64_t>(S::kBN) * args.ldb * 2 < gemm::kMaxSpan) {
-            return launch<std::uint16_t, 4, 2, 2, 3, 64, 2, true, true, true>(
+            return launch<std::uint16_t, 4, 3, 2, 2, 64, 3, true, true, true>(
                 a, b, bias, c, args, vector_output(c, args), stream);
         }
     }

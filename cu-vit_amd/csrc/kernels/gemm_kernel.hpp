@@ -9,16 +9,15 @@
 // (entry * stride) or split into (entry / inner, entry % inner) with outer
 // strides (gemm.cu:58-72); every operand has its own leading dimension.
 //
-// Structure. A workgroup of WM x WN wavefronts (four, or eight for the
-// largest bf16 tiles) owns a BM x BN tile of C; each
+// Structure. A workgroup of WM x WN wavefronts (four, or twelve for the
+// largest bf16 tile) owns a BM x BN tile of C; each
 // wavefront owns (TM * E) x (TN * E) of it as TM x TN MFMA tiles of edge E.
 // K is walked in BK-wide stages. Both operand tiles sit in LDS as
 // [rows][BK] (k contiguous), rows padded by 16 bytes so that the sixteen
 // lanes reading one fragment column hit sixteen different bank quads. Stages
 // are double-buffered in LDS and fetched from global memory into registers
 // two stages ahead, so a global load has two stages of MFMA work to land and
-// each stage costs one barrier (one stage ahead for eight wavefronts with
-// 64-deep stages, whose registers hold one stage's fetch, not two).
+// each stage costs one barrier.
 //
 // MFMA. fp32 uses v_mfma_f32_16x16x4_f32 (E = 16) and bf16
 // v_mfma_f32_32x32x16_bf16 (E = 32); measured on MI355X with an in-kernel
@@ -233,7 +232,7 @@ __device__ __forceinline__ void store4(std::uint16_t* p, const float (&value)[4]
 
 /// Compile-time shape of one kernel instance.
 template <typename T, int WM, int WN, int TM, int TN, int BK> struct Shape {
-    static_assert(WM * WN == 4 || WM * WN == 8, "four or eight wavefronts per workgroup");
+    static_assert(WM * WN == 4 || WM * WN == 12, "four or twelve wavefronts per workgroup");
     static constexpr int kThreads = kWave * WM * WN;
     static constexpr int kE = Mma<T>::kEdge;
     static constexpr int kBM = WM * TM * kE;
@@ -529,23 +528,7 @@ __global__ __launch_bounds__(kWave * WM * WN) __attribute__((amdgpu_waves_per_eu
         // that started at +0, which changes no bit of them. So every path
         // through the loop has the same loads in flight, each LDS write waits
         // only for its own set, and the accumulators stay in place.
-        // Eight wavefronts of 64-deep stages run with one register set: at two
-        // wavefronts per SIMD a lane has 256 registers, and a second set of
-        // the stage's fetch (28 of them) spills. A stage's loads are then
-        // issued during the stage before it and written to LDS at its end.
-        constexpr bool kOneSet = S::kThreads == 512 && BK == 64;
-        if (kOneSet && steps > 0) {
-            fetch(ra0, rb0, 0);
-            stage(ra0, rb0, 0);
-            fetch(ra0, rb0, 1);
-            __syncthreads();
-            for (int step = 0; step < steps; step += 2) {
-                advance(ra0, rb0, ra0, rb0, 0, step + 2);
-                __syncthreads();
-                advance(ra0, rb0, ra0, rb0, 1, step + 3);
-                __syncthreads();
-            }
-        } else if (steps > 0) {
+        if (steps > 0) {
             fetch(ra0, rb0, 0);
             stage(ra0, rb0, 0);
             fetch(ra1, rb1, 1);

@@ -1,8 +1,9 @@
-"""The eight-wavefront bf16 GEMM tile (256 x 192, wavefront tiles of 64 x 96,
-64-deep stages), which long products with B as [N, K] take when one round of
-such tiles covers the problem and 128 x 128 tiles would need more than two per
-compute unit: the ViT-Base FC2 at batch 64 (12608 x 768 x 3072, accumulating
-into the residual stream).
+"""The twelve-wavefront bf16 GEMM tile (256 x 192, wavefront tiles of 64 x 64,
+64-deep stages), which products with B as [N, K] and K of at least 512 take
+when one round of such tiles covers the problem and 128 x 128 tiles would need
+more than two per compute unit: the ViT-Base FC2 and projection at batch 64
+(12608 x 768 x 3072 and 12608 x 768 x 768, accumulating into the residual
+stream).
 
 Its results must be bitwise those of the 64 x 64 kernel that small problems
 take: both run the same MFMA over the same k-blocks in the same order and
@@ -48,8 +49,10 @@ def require_gemm_close(actual, expected, scale, context):
 CASES = [
     # m, n, k, bias, gelu, accumulate, alpha, lda pad, ldc pad
     (12608, 768, 3072, True, False, True, 1.0, 0, 0),      # ViT-Base FC2 into the residual
-    (12000, 760, 2100, True, True, True, 0.75, 8, 8),      # M, N and K tails, GELU + accumulate
+    (12000, 760, 2104, True, True, True, 0.75, 8, 8),      # M, N and K tails, GELU + accumulate
     (11008, 768, 2048, False, False, False, -1.25, 0, 0),  # no bias, no accumulation
+    (12608, 768, 768, True, False, True, 1.0, 0, 0),       # ViT-Base projection
+    (12300, 736, 520, True, True, False, 2.0, 0, 8),       # short K with a tail, N tail, GELU
 ]
 
 
