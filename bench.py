@@ -386,7 +386,8 @@ def vit_forward(torch, cuvit, device, batch: int, replays: int, base: bool = Fal
 def vit_base_bf16(torch, cuvit, device):
     """ViT-Base/16 batch-64 shapes with bf16 activations: cold per-launch times
     of LN [12608, 768], softmax [151296, 197] in place, the patch gather
-    [64, 3, 224, 224] and FC1 with the GELU epilogue (M 12608, N 3072, K 768)."""
+    [64, 3, 224, 224], FC1 with the GELU epilogue (M 12608, N 3072, K 768) and
+    FC2 accumulating into the residual stream (M 12608, N 768, K 3072)."""
     rows, embed, hidden, heads, batch = 64 * TOKENS, 768, 3072, 12, 64
     bf = torch.bfloat16
     results = {}
@@ -434,6 +435,16 @@ def vit_base_bf16(torch, cuvit, device):
     flops = 2.0 * rows * hidden * embed
     results["fc1_gelu_gemm"]["TFLOPs"] = round(flops / (ms * 1e-3) / 1e12, 2)
     results["fc1_gelu_gemm"]["frac_of_bf16_mfma_peak"] = round(flops / (ms * 1e-3) / 2.5e15, 4)
+    del a, c
+    # FC2 accumulating into the residual stream (M 12608, N 768, K 3072).
+    h = [torch.randn(rows * hidden, device=device).to(bf) for _ in range(2)]
+    residual = [torch.randn(rows * embed, device=device).to(bf) for _ in range(2)]
+    fc2 = cuvit.gemm_problem(rows, embed, hidden, cuvit.TRANSPOSED)
+    fc2.epilogue.accumulate = 1
+    ms = record("fc2_gemm", 2 * (rows * hidden + embed * hidden + 2 * rows * embed),
+                lambda i: cuvit.gemm(h[i], w, bias, residual[i], fc2), 2)
+    results["fc2_gemm"]["TFLOPs"] = round(flops / (ms * 1e-3) / 1e12, 2)
+    results["fc2_gemm"]["frac_of_bf16_mfma_peak"] = round(flops / (ms * 1e-3) / 2.5e15, 4)
     return results
 
 
