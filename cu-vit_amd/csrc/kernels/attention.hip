@@ -16,7 +16,7 @@
 //     t + 16 j in order from +0, then the DPP tree (pair, quad, half-row
 //     mirror, row mirror). Here the 16 partial sums sit four to a lane in
 //     the four lanes that hold a query row, and the tree is replayed with
-//     two cross-lane exchanges; probabilities are e * (1 / sum) as there;
+//     two cross-lane swaps; probabilities are e * (1 / sum) as there;
 //   * weights.V: the GEMM's MFMA over keys in k-blocks of 16, keys past the
 //     token count contributing exact zeros.
 // The probabilities never leave registers: a lane of the logits tile holds
@@ -46,8 +46,23 @@ constexpr int kPitch = kHeadDim + 4;  // floats per LDS row
 constexpr int kMaxKeyTiles = 16;      // up to 256 tokens
 constexpr float kLog2e = 1.4426950408889634F;
 
-__device__ __forceinline__ float shuffle_xor(float value, int mask) {
-    return __shfl_xor(value, mask, kWave);
+/// op(value of lanes 16 k + i, value of lanes 16 (k + 1) + i) for k = 0 and
+/// k = 2, in both lanes of each pair (@p kRows 16: rows of 16 lanes, by
+/// v_permlane16_swap), or op(lower half, upper half) (@p kRows 32, by
+/// v_permlane32_swap): a swap of the value with itself leaves each lane its
+/// own value and its partner's, the lower one first in both lanes, with no LDS
+/// round trip. op is max or + here, which give the same bits as
+/// op(own, partner) in either order.
+template <int kRows, typename Op> __device__ __forceinline__ float combine_rows(float value, Op op) {
+    const std::uint32_t bits = __float_as_uint(value);
+    if constexpr (kRows == 16) {
+        const auto swapped = __builtin_amdgcn_permlane16_swap(bits, bits, false, false);
+        return op(__uint_as_float(swapped[0]), __uint_as_float(swapped[1]));
+    } else {
+        static_assert(kRows == 32, "rows of 16 or halves of 32 lanes");
+        const auto swapped = __builtin_amdgcn_permlane32_swap(bits, bits, false, false);
+        return op(__uint_as_float(swapped[0]), __uint_as_float(swapped[1]));
+    }
 }
 
 template <int KT, int Waves>
@@ -151,8 +166,8 @@ __global__ __launch_bounds__(Waves * kWave) void attention_kernel(const float* _
             }
         }
     }
-    maximum = fmaxf(maximum, shuffle_xor(maximum, 16));
-    maximum = fmaxf(maximum, shuffle_xor(maximum, 32));
+    const auto larger = [](float a, float b) { return fmaxf(a, b); };
+    maximum = combine_rows<32>(combine_rows<16>(maximum, larger), larger);
 
     // Exponentials; keys past the tokens become exact zeros.
 #pragma unroll
@@ -182,8 +197,8 @@ __global__ __launch_bounds__(Waves * kWave) void attention_kernel(const float* _
         partial[r] = sum;
     }
     const float quad = (partial[0] + partial[1]) + (partial[2] + partial[3]);
-    const float half = quad + shuffle_xor(quad, 16);
-    const float inverse = 1.0F / (half + shuffle_xor(half, 32));
+    const auto add = [](float a, float b) { return a + b; };
+    const float inverse = 1.0F / combine_rows<32>(combine_rows<16>(quad, add), add);
 #pragma unroll
     for (int jt = 0; jt < KT; ++jt) {
 #pragma unroll

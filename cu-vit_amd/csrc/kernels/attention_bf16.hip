@@ -30,7 +30,7 @@
 // 4 (l / 32) + r of a lane's runs: each lane keeps eight of the sixteen
 // partial sums in the same order, the DPP tree (t ^ 1, t ^ 2, half-row
 // mirror, row mirror) becomes (Q0 + Q1) + (Q2 + Q3) over the quad totals Qa
-// with one exchange between l and l ^ 32, and the probabilities, rounded to
+// with one swap between l and l ^ 32, and the probabilities, rounded to
 // bf16, are swapped by halves between l and l ^ 32 into the weights.V A
 // fragments (8 consecutive keys per lane).
 //
@@ -132,7 +132,17 @@ __device__ __forceinline__ Vec16 load_or_zero(__amdgpu_buffer_rsrc_t resource, s
     return gemm::buffer_load16(resource, inside ? static_cast<unsigned int>(element * 2) : gemm::kOutside);
 }
 
-__device__ __forceinline__ float exchange(float value) { return __shfl_xor(value, 32, kWave); }
+/// op(the lower half's value, the upper half's value) in lanes l and l ^ 32
+/// alike: one v_permlane32_swap of the value with itself leaves a lane of the
+/// lower half its own value and its partner's, and a lane of the upper half
+/// its partner's and its own, lower half first in both (no LDS round trip).
+/// The two halves then hold the same bits; op is max or + here, which give
+/// the same bits as op(own, partner) in either order.
+template <typename Op> __device__ __forceinline__ float combine_halves(float value, Op op) {
+    const std::uint32_t bits = __float_as_uint(value);
+    const auto swapped = __builtin_amdgcn_permlane32_swap(bits, bits, false, false);
+    return op(__uint_as_float(swapped[0]), __uint_as_float(swapped[1]));
+}
 
 __device__ __forceinline__ std::uint32_t pack_bf16(float low, float high) {
     return pack_bf16x2(low, high);
@@ -315,7 +325,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
         }
     }
     maximum = bf16_to_float(float_to_bf16(maximum));
-    maximum = fmaxf(maximum, exchange(maximum));
+    maximum = combine_halves(maximum, [](float a, float b) { return fmaxf(a, b); });
 
     // Exponentials; keys past the tokens are 0, as the softmax sets them.
 #pragma unroll
@@ -349,7 +359,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
     }
     // half-row mirror pairs quads 0-1 and 2-3, row mirror the two results:
     // (Q0 + Q1) + (Q2 + Q3), the same bits in both lanes of the row
-    const float total = (quad[0] + exchange(quad[0])) + (quad[1] + exchange(quad[1]));
+    const auto add = [](float a, float b) { return a + b; };
+    const float total = combine_halves(quad[0], add) + combine_halves(quad[1], add);
     const float inverse = 1.0F / total;
 
     // Probabilities rounded to bf16 and packed by runs: p[kt][q] = keys
