@@ -344,27 +344,34 @@ int gemm_bf16_with_addend(const std::uint16_t* a, const std::uint16_t* b, const 
 }
 
 int layer_norm_cached(const float* input, const float* gamma, const float* beta, float* output,
-                      int rows, int columns, float epsilon, hipStream_t stream) {
+                      int rows, int columns, float epsilon, hipStream_t stream,
+                      std::int64_t input_stride) {
     bool empty = false;
     if (const int s = check_layer_norm(input, gamma, beta, output, rows, columns, &empty);
         s != CUVIT_OK || empty) {
         return s;
     }
+    if (input_stride != 0 && input_stride < columns) {
+        return fail(CUVIT_ERROR_INVALID_ARGUMENT, "layer_norm rows overlap");
+    }
     return from_hip(detail::layer_norm_f32(input, gamma, beta, output, rows, columns, epsilon,
-                                           stream, false),
+                                           stream, false, input_stride),
                     "layer_norm launch");
 }
 
 int layer_norm_cached(const std::uint16_t* input, const float* gamma, const float* beta,
                       std::uint16_t* output, int rows, int columns, float epsilon,
-                      hipStream_t stream) {
+                      hipStream_t stream, std::int64_t input_stride) {
     bool empty = false;
     if (const int s = check_layer_norm(input, gamma, beta, output, rows, columns, &empty);
         s != CUVIT_OK || empty) {
         return s;
     }
+    if (input_stride != 0 && input_stride < columns) {
+        return fail(CUVIT_ERROR_INVALID_ARGUMENT, "layer_norm rows overlap");
+    }
     return from_hip(detail::layer_norm_bf16(input, gamma, beta, output, rows, columns, epsilon,
-                                            stream, false),
+                                            stream, false, input_stride),
                     "layer_norm launch");
 }
 

@@ -44,11 +44,14 @@ int gemm_bf16_with_addend(const std::uint16_t* a, const std::uint16_t* b, const 
 /// caller whose next launch reads the output: the model's blocks, where the
 /// normalised rows feed a GEMM at once. Same validation and values as the C
 /// ABI's entry points, which store non-temporally.
+/// Input rows sit @p input_stride elements apart (0: packed); output rows are
+/// packed.
 int layer_norm_cached(const float* input, const float* gamma, const float* beta, float* output,
-                      int rows, int columns, float epsilon, hipStream_t stream);
+                      int rows, int columns, float epsilon, hipStream_t stream,
+                      std::int64_t input_stride = 0);
 int layer_norm_cached(const std::uint16_t* input, const float* gamma, const float* beta,
                       std::uint16_t* output, int rows, int columns, float epsilon,
-                      hipStream_t stream);
+                      hipStream_t stream, std::int64_t input_stride = 0);
 
 /// The checks of preprocess (image.cpp:96-104, 126-128), in its order: an
 /// empty image, a non-positive size, a crop fraction outside (0, 1], a zero

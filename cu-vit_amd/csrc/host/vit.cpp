@@ -497,15 +497,16 @@ void VisionTransformer::forward_stored(Stored<T>& stored, const float* images, f
         run_block<T>(blocks_[index], stored.blocks[index], stored, batch, stream);
     }
 
+    // Class-token pooling: only row 0 of each image feeds the head, so the
+    // final LayerNorm normalizes those rows alone (tokens_per_image apart, into
+    // [batch, embed]) and the head is one [batch, embed] x [classes, embed]^T
+    // product. Each row is computed by the same operations as in the
+    // reference's LayerNorm over every token followed by its batch of
+    // one-row head GEMMs (vit.cu:305-316), so the logits are the same bits.
     throw_on_error(capi::layer_norm_cached(stored.tokens, final_gamma_, final_beta_,
-                                           stored.normalized, batch * token_count, embed,
-                                           config_.layer_norm_epsilon, stream));
-
-    // Class-token pooling: one row per image feeds the head.
-    GemmProblem head = gemm_problem(1, config_.classes, embed, GemmLayout::kTransposed);
-    head.batch.count = batch;
-    head.batch.stride_a = tokens_per_image;
-    head.batch.stride_c = config_.classes;
+                                           stored.normalized, batch, embed,
+                                           config_.layer_norm_epsilon, stream, tokens_per_image));
+    GemmProblem head = gemm_problem(batch, config_.classes, embed, GemmLayout::kTransposed);
     if constexpr (kFloat) {
         launch_gemm(stored.normalized, stored.head_weight, head_bias_, logits, head, stream);
     } else {

@@ -26,13 +26,16 @@ hipError_t preprocess_u8(const std::uint8_t* pixels, int batch, int width, int h
 
 // layer_norm.hip. With @p streaming the output is stored non-temporally
 // (best when it is read back from HBM later); without, it stays in the
-// caches for a kernel that reads it next. The values are the same.
+// caches for a kernel that reads it next. The values are the same. Input
+// rows sit @p input_stride elements apart (0: packed, @p columns); output
+// rows are packed.
 hipError_t layer_norm_f32(const float* input, const float* gamma, const float* beta, float* output,
                           int rows, int columns, float epsilon, hipStream_t stream,
-                          bool streaming = true);
+                          bool streaming = true, std::int64_t input_stride = 0);
 hipError_t layer_norm_bf16(const std::uint16_t* input, const float* gamma, const float* beta,
                            std::uint16_t* output, int rows, int columns, float epsilon,
-                           hipStream_t stream, bool streaming = true);
+                           hipStream_t stream, bool streaming = true,
+                           std::int64_t input_stride = 0);
 
 // softmax.hip
 hipError_t softmax_f32(const float* input, float* output, int rows, int columns,

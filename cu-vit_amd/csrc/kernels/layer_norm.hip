@@ -52,10 +52,13 @@ __device__ __forceinline__ float lane_broadcast(float v, int source_lane) {
 /// @tparam kColumns the row width when it is fixed at compile time (the ViT
 /// widths), 0 otherwise: the width's divisions, the column masks and the row
 /// offsets then fold to constants ahead of the first load, the same values.
-template <typename T, int Lanes, int V, bool Streaming, int kColumns = 0>
+/// @tparam Strided input rows @p input_stride elements apart; otherwise packed
+/// (the stride is the row width, compile-time with @p kColumns).
+template <typename T, int Lanes, int V, bool Streaming, int kColumns = 0, bool Strided = false>
 __global__ __launch_bounds__(kBlock) void layer_norm_vector_kernel(
     const T* __restrict__ input, const float* __restrict__ gamma, const float* __restrict__ beta,
-    T* __restrict__ output, int rows, int columns_argument, float epsilon) {
+    T* __restrict__ output, int rows, int columns_argument, float epsilon,
+    std::int64_t input_stride) {
     constexpr int E = Elem<T>::kPerVec;
     const int columns = kColumns > 0 ? kColumns : columns_argument;
     constexpr int kTeams = kWave / Lanes;
@@ -111,7 +114,7 @@ __global__ __launch_bounds__(kBlock) void layer_norm_vector_kernel(
     for (std::int64_t group = first_wave; group < groups; group += wave_count) {
         const std::int64_t row = group * kTeams + team;
         const bool row_valid = row < rows;
-        const T* const source = input + row * columns;
+        const T* const source = input + row * (Strided ? input_stride : columns);
 
         Vec16 raw[V];
 #pragma unroll
@@ -192,7 +195,7 @@ __global__ __launch_bounds__(kBlock) void layer_norm_vector_kernel(
 template <typename T>
 __global__ __launch_bounds__(kBlock) void layer_norm_generic_kernel(
     const T* __restrict__ input, const float* __restrict__ gamma, const float* __restrict__ beta,
-    T* __restrict__ output, int rows, int columns, float epsilon) {
+    T* __restrict__ output, int rows, int columns, float epsilon, std::int64_t input_stride) {
     const int lane = lane_id();
     const float inverse_columns = 1.0F / static_cast<float>(columns);
     const std::int64_t wave_count = static_cast<std::int64_t>(gridDim.x) * kWavesPerBlock;
@@ -200,7 +203,7 @@ __global__ __launch_bounds__(kBlock) void layer_norm_generic_kernel(
     for (std::int64_t row = static_cast<std::int64_t>(blockIdx.x) * kWavesPerBlock +
                             threadIdx.x / kWave;
          row < rows; row += wave_count) {
-        const T* const source = input + row * columns;
+        const T* const source = input + row * input_stride;
         const float x0 = Elem<T>::load(source);
 
         float partial = 0.F;
@@ -229,78 +232,100 @@ __global__ __launch_bounds__(kBlock) void layer_norm_generic_kernel(
 /// Waves each compute unit is given before the kernels start looping.
 constexpr int kWavesPerCu = 16;
 
-template <typename T, int Lanes, int V, int kColumns = 0>
+template <typename T, int Lanes, int V, int kColumns = 0, bool Strided = false>
 hipError_t launch_vector(const T* input, const float* gamma, const float* beta, T* output, int rows,
-                         int columns, float epsilon, bool streaming, hipStream_t stream) {
+                         int columns, float epsilon, bool streaming, std::int64_t input_stride,
+                         hipStream_t stream) {
     constexpr int kTeams = kWave / Lanes;
     const std::int64_t groups = (static_cast<std::int64_t>(rows) + kTeams - 1) / kTeams;
     const unsigned int grid = stride_grid(groups, kWavesPerBlock, kWavesPerCu / kWavesPerBlock);
-    auto kernel = streaming ? layer_norm_vector_kernel<T, Lanes, V, true, kColumns>
-                            : layer_norm_vector_kernel<T, Lanes, V, false, kColumns>;
-    kernel<<<grid, kBlock, 0, stream>>>(input, gamma, beta, output, rows, columns, epsilon);
+    auto kernel = streaming ? layer_norm_vector_kernel<T, Lanes, V, true, kColumns, Strided>
+                            : layer_norm_vector_kernel<T, Lanes, V, false, kColumns, Strided>;
+    kernel<<<grid, kBlock, 0, stream>>>(input, gamma, beta, output, rows, columns, epsilon,
+                                        input_stride);
     return hipGetLastError();
 }
 
 template <typename T>
 hipError_t dispatch(const T* input, const float* gamma, const float* beta, T* output, int rows,
-                    int columns, float epsilon, bool streaming, hipStream_t stream) {
+                    int columns, float epsilon, bool streaming, std::int64_t input_stride,
+                    hipStream_t stream) {
     constexpr int E = Elem<T>::kPerVec;
-    const bool vectorizable = columns % E == 0 && aligned16(input) && aligned16(output) &&
-                              aligned16(gamma) && aligned16(beta);
+    const bool vectorizable = columns % E == 0 && input_stride % E == 0 && aligned16(input) &&
+                              aligned16(output) && aligned16(gamma) && aligned16(beta);
     const int vectors = columns / E;
+    if (input_stride != columns) {
+        // Strided rows (the model's class-token rows): the ViT widths, else
+        // the one-wavefront-per-row kernel.
+        if (vectorizable && columns == 192) {
+            return launch_vector<T, 16, (192 / E + 15) / 16, 192, true>(
+                input, gamma, beta, output, rows, columns, epsilon, streaming, input_stride, stream);
+        }
+        if (vectorizable && columns == 768) {
+            constexpr int kLanes = 768 / E <= 16 * 8 ? 16 : kWave;
+            return launch_vector<T, kLanes, (768 / E + kLanes - 1) / kLanes, 768, true>(
+                input, gamma, beta, output, rows, columns, epsilon, streaming, input_stride, stream);
+        }
+        const unsigned int grid = stride_grid(rows, kWavesPerBlock, kWavesPerCu / kWavesPerBlock);
+        layer_norm_generic_kernel<T><<<grid, kBlock, 0, stream>>>(input, gamma, beta, output, rows,
+                                                                  columns, epsilon, input_stride);
+        return hipGetLastError();
+    }
     // The ViT widths with the width fixed at compile time, each on the team and
     // vector count the switch below picks ([6304, 192] fp32 3.37 -> 3.31 us,
     // [12608, 768] bf16 9.36 -> 8.56 us).
     if (vectorizable && columns == 192) {
         return launch_vector<T, 16, (192 / E + 15) / 16, 192>(input, gamma, beta, output, rows, columns,
-                                                              epsilon, streaming, stream);
+                                                              epsilon, streaming, input_stride, stream);
     }
     if (vectorizable && columns == 768) {
         constexpr bool kNarrow = 768 / E <= 16 * 8;
         constexpr int kLanes = kNarrow ? 16 : kWave;
         return launch_vector<T, kLanes, (768 / E + kLanes - 1) / kLanes, 768>(
-            input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
+            input, gamma, beta, output, rows, columns, epsilon, streaming, input_stride, stream);
     }
     if (vectorizable && vectors <= 16 * 8) {
         switch ((vectors + 15) / 16) {
-        case 1: return launch_vector<T, 16, 1>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
-        case 2: return launch_vector<T, 16, 2>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
-        case 3: return launch_vector<T, 16, 3>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
-        case 4: return launch_vector<T, 16, 4>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
-        case 5: return launch_vector<T, 16, 5>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
-        case 6: return launch_vector<T, 16, 6>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
-        case 7: return launch_vector<T, 16, 7>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
-        default: return launch_vector<T, 16, 8>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
+        case 1: return launch_vector<T, 16, 1>(input, gamma, beta, output, rows, columns, epsilon, streaming, input_stride, stream);
+        case 2: return launch_vector<T, 16, 2>(input, gamma, beta, output, rows, columns, epsilon, streaming, input_stride, stream);
+        case 3: return launch_vector<T, 16, 3>(input, gamma, beta, output, rows, columns, epsilon, streaming, input_stride, stream);
+        case 4: return launch_vector<T, 16, 4>(input, gamma, beta, output, rows, columns, epsilon, streaming, input_stride, stream);
+        case 5: return launch_vector<T, 16, 5>(input, gamma, beta, output, rows, columns, epsilon, streaming, input_stride, stream);
+        case 6: return launch_vector<T, 16, 6>(input, gamma, beta, output, rows, columns, epsilon, streaming, input_stride, stream);
+        case 7: return launch_vector<T, 16, 7>(input, gamma, beta, output, rows, columns, epsilon, streaming, input_stride, stream);
+        default: return launch_vector<T, 16, 8>(input, gamma, beta, output, rows, columns, epsilon, streaming, input_stride, stream);
         }
     }
     if (vectorizable && vectors <= kWave * 8) {
         switch ((vectors + kWave - 1) / kWave) {
-        case 3: return launch_vector<T, 64, 3>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
-        case 4: return launch_vector<T, 64, 4>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
-        case 5: return launch_vector<T, 64, 5>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
-        case 6: return launch_vector<T, 64, 6>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
-        case 7: return launch_vector<T, 64, 7>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
-        default: return launch_vector<T, 64, 8>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
+        case 3: return launch_vector<T, 64, 3>(input, gamma, beta, output, rows, columns, epsilon, streaming, input_stride, stream);
+        case 4: return launch_vector<T, 64, 4>(input, gamma, beta, output, rows, columns, epsilon, streaming, input_stride, stream);
+        case 5: return launch_vector<T, 64, 5>(input, gamma, beta, output, rows, columns, epsilon, streaming, input_stride, stream);
+        case 6: return launch_vector<T, 64, 6>(input, gamma, beta, output, rows, columns, epsilon, streaming, input_stride, stream);
+        case 7: return launch_vector<T, 64, 7>(input, gamma, beta, output, rows, columns, epsilon, streaming, input_stride, stream);
+        default: return launch_vector<T, 64, 8>(input, gamma, beta, output, rows, columns, epsilon, streaming, input_stride, stream);
         }
     }
     const unsigned int grid = stride_grid(rows, kWavesPerBlock, kWavesPerCu / kWavesPerBlock);
-    layer_norm_generic_kernel<T>
-        <<<grid, kBlock, 0, stream>>>(input, gamma, beta, output, rows, columns, epsilon);
+    layer_norm_generic_kernel<T><<<grid, kBlock, 0, stream>>>(input, gamma, beta, output, rows,
+                                                              columns, epsilon, input_stride);
     return hipGetLastError();
 }
 
 } // namespace
 
 hipError_t layer_norm_f32(const float* input, const float* gamma, const float* beta, float* output,
-                          int rows, int columns, float epsilon, hipStream_t stream, bool streaming) {
-    return dispatch<float>(input, gamma, beta, output, rows, columns, epsilon, streaming, stream);
+                          int rows, int columns, float epsilon, hipStream_t stream, bool streaming,
+                          std::int64_t input_stride) {
+    return dispatch<float>(input, gamma, beta, output, rows, columns, epsilon, streaming,
+                           input_stride > 0 ? input_stride : columns, stream);
 }
 
 hipError_t layer_norm_bf16(const std::uint16_t* input, const float* gamma, const float* beta,
                            std::uint16_t* output, int rows, int columns, float epsilon,
-                           hipStream_t stream, bool streaming) {
+                           hipStream_t stream, bool streaming, std::int64_t input_stride) {
     return dispatch<std::uint16_t>(input, gamma, beta, output, rows, columns, epsilon, streaming,
-                                   stream);
+                                   input_stride > 0 ? input_stride : columns, stream);
 }
 
 } // namespace cuvit::detail
