@@ -552,7 +552,15 @@ __global__ __launch_bounds__(kWave * WM * WN) __attribute__((amdgpu_waves_per_eu
             if (row >= args.m) {
                 continue;
             }
-            T* const c_row = c_entry + static_cast<std::int64_t>(row) * args.ldc;
+            // Batch entries run as one problem: the entry's own row.
+            int local = row;
+            std::int64_t c_offset = static_cast<std::int64_t>(row) * args.ldc;
+            if (args.rows_per_entry > 0) {
+                const int entry_index = row / args.rows_per_entry;
+                local = row - entry_index * args.rows_per_entry;
+                c_offset = entry_index * args.stride_c + static_cast<std::int64_t>(local) * args.ldc;
+            }
+            T* const c_row = c_entry + c_offset;
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
 #pragma unroll
@@ -565,7 +573,7 @@ __global__ __launch_bounds__(kWave * WM * WN) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         value[r] = col + r < args.n
-                                       ? epilogue_value(acc[i][j][4 * q + r], bias, row, col + r, args)
+                                       ? epilogue_value(acc[i][j][4 * q + r], bias, local, col + r, args)
                                        : 0.F;
                     }
                     if (vector_c && col + 3 < args.n) {

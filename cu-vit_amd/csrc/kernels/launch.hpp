@@ -93,6 +93,12 @@ struct GemmArgs {
     /// patch-embedding GEMM.
     const float* addend = nullptr;
     int ld_addend = 0;
+    /// When > 0, the m rows are consecutive batch entries of rows_per_entry
+    /// rows each, run as one problem (A rows contiguous across the entries,
+    /// count 1): output row p is row p % rows_per_entry of entry
+    /// p / rows_per_entry, stored at entry * stride_c, and its addend row is
+    /// p % rows_per_entry. Set by the dispatch only, for the tile that takes it.
+    int rows_per_entry = 0;
 };
 
 hipError_t gemm_f32(const float* a, const float* b, const float* bias, float* c,

@@ -123,3 +123,28 @@ def test_tall_tile_batched_entries(cuvit, oracle, device):
         one = bf16_tensor(c_bits[entry * m * n:(entry + 1) * m * n], device)
         cuvit.gemm(da[entry * m * k:], dw, bias, one, single)
         require_exact(bf16_bits(one).reshape(m, n), both[entry], f"batch entry {entry}")
+
+
+def test_tall_tile_runs_a_shared_weight_batch_as_one_problem(cuvit, oracle, device):
+    """A batch of 64 entries of 196 rows with B shared and A rows following
+    one another (the ViT-Base patch embedding's shape) runs as one problem of
+    12544 rows on the tall tile; each entry lands at its own C stride (197
+    rows apart, so one row per entry is never written) and equals its own
+    launch of 196 rows, bit for bit."""
+    entries, m, n, k = 64, 196, 768, 768
+    a_bits, _ = bf16_inputs(oracle, 95, entries * m * k)
+    w_bits, _ = bf16_inputs(oracle, 96, n * k, 0.02)
+    c_bits, _ = bf16_inputs(oracle, 97, entries * (m + 1) * n)
+    bias = to_device(oracle.generator(98).normal(n, 0.0, 0.5), device)
+    da, dw = bf16_tensor(a_bits, device), bf16_tensor(w_bits, device)
+    p = cuvit.gemm_problem(m, n, k, cuvit.TRANSPOSED)
+    p.batch.count, p.batch.stride_a, p.batch.stride_b, p.batch.stride_c = entries, m * k, 0, (m + 1) * n
+    c = bf16_tensor(c_bits, device)
+    cuvit.gemm(da, dw, bias, c, p)
+    full = bf16_bits(c).reshape(entries, m + 1, n)
+    require_exact(full[:, m], c_bits.reshape(entries, m + 1, n)[:, m], "the rows between entries changed")
+    single = cuvit.gemm_problem(m, n, k, cuvit.TRANSPOSED)
+    one = torch.empty(m * n, dtype=torch.bfloat16, device=device)
+    for entry in (0, 1, 31, 63):
+        cuvit.gemm(da[entry * m * k:], dw, bias, one, single)
+        require_exact(bf16_bits(one).reshape(m, n), full[entry, :m], f"batch entry {entry}")
