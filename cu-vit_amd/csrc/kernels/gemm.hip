@@ -135,6 +135,22 @@ hipError_t pick_flags(const T* a, const T* b, const float* bias, T* c, const Gem
 #undef CUVIT_GEMM_LAUNCH
 }
 
+/// @p args with a batch whose entries share B (stride 0) and whose A rows
+/// follow one another run as one problem of all the entries' rows
+/// (rows_per_entry: each output row goes back to its entry); @p args itself
+/// otherwise. Every output is computed by the same operations either way.
+GemmArgs as_one_problem(const GemmArgs& args) {
+    GemmArgs whole = args;
+    if (args.count > 1 && args.inner == 0 && args.stride_b == 0 && args.m > 0 &&
+        args.stride_a == static_cast<std::int64_t>(args.m) * args.lda &&
+        static_cast<std::int64_t>(args.m) * args.count <= 0x7FFFFFFF) {
+        whole.m = args.m * args.count;
+        whole.count = 1;
+        whole.rows_per_entry = args.m;
+    }
+    return whole;
+}
+
 std::int64_t tile_count(const GemmArgs& args, int bm, int bn) {
     return static_cast<std::int64_t>((args.m + bm - 1) / bm) * ((args.n + bn - 1) / bn) * args.count;
 }
@@ -142,22 +158,32 @@ std::int64_t tile_count(const GemmArgs& args, int bm, int bn) {
 } // namespace
 
 /// The resident-panel kernel (gemm_panel.hpp) for a problem it covers: one
-/// batch entry, B as [N, K], K equal to 16 KB, vector A and
-/// B, C written in 16-byte runs (N, ldc multiples of 4, C 16-byte aligned), no
-/// addend, every operand within one descriptor's span, and at least eight
-/// wavefront items per compute unit. Returns hipErrorNotSupported otherwise.
+/// batch entry (or entries run as one, rows_per_entry), B as [N, K], K equal
+/// to 16 KB, vector A and B, C written in 16-byte runs (N, ldc and the entry
+/// stride multiples of 4, C 16-byte aligned), an addend only without GELU or
+/// accumulation (and in 16-byte runs), every operand within one descriptor's
+/// span, and at least eight wavefront items per compute unit. Returns
+/// hipErrorNotSupported otherwise.
 template <int KB, int BN, int TN, int KG, int W>
 hipError_t launch_panel(const float* a, const float* b, const float* bias, float* c,
                         const GemmArgs& args, hipStream_t stream) {
     using S = gemm::PanelShape<KB, BN, TN, KG, W>;
     const std::int64_t tiles_m = (args.m + 15) / 16;
     const std::int64_t panels = (args.n + BN - 1) / BN;
+    const bool with_addend = args.addend != nullptr;
+    const std::int64_t c_span =
+        args.rows_per_entry > 0
+            ? ((args.m - 1) / args.rows_per_entry + 1) * args.stride_c
+            : static_cast<std::int64_t>(args.m) * args.ldc;
     const bool eligible =
-        args.count == 1 && args.transposed && args.addend == nullptr &&
+        args.count == 1 && args.transposed &&
+        (!with_addend || (!args.gelu && !args.accumulate && aligned16(args.addend) &&
+                          args.ld_addend % 4 == 0 &&
+                          static_cast<std::int64_t>(args.m) * args.ld_addend * 4 < gemm::kMaxSpan)) &&
         args.k == 16 * KB && vector_operand(a, args.lda, args.k, 0, 0, false) &&
         vector_operand(b, args.ldb, args.k, 0, 0, false) && vector_output(c, args) && aligned16(c) &&
         args.n % 4 == 0 && static_cast<std::int64_t>(args.m) * args.lda * 4 < gemm::kMaxSpan &&
-        static_cast<std::int64_t>(args.m) * args.ldc * 4 < gemm::kMaxSpan &&
+        c_span * 4 < gemm::kMaxSpan &&
         static_cast<std::int64_t>(BN) * args.ldb * 4 < gemm::kMaxSpan &&
         tiles_m * panels * S::kParts >= 8 * static_cast<std::int64_t>(compute_units());
     if (!eligible) {
@@ -180,12 +206,21 @@ hipError_t launch_panel(const float* a, const float* b, const float* bias, float
         return hipGetLastError();
     };
     // The epilogue's parts as template flags: alpha (when not 1), bias, GELU,
-    // accumulate.
+    // accumulate; the addend alone (the patch embedding's positional add).
     auto with_alpha = [&](auto alpha, auto with_bias, auto gelu, auto accumulate) -> hipError_t {
         return run(gemm::gemm_panel_kernel<KB, BN, TN, KG, W, decltype(alpha)::value,
                                            decltype(with_bias)::value, decltype(gelu)::value,
                                            decltype(accumulate)::value>);
     };
+    if (with_addend) {
+        auto with_bias = [&](auto alpha) -> hipError_t {
+            constexpr bool kAlpha = decltype(alpha)::value;
+            return bias != nullptr
+                       ? run(gemm::gemm_panel_kernel<KB, BN, TN, KG, W, kAlpha, true, false, false, true>)
+                       : run(gemm::gemm_panel_kernel<KB, BN, TN, KG, W, kAlpha, false, false, false, true>);
+        };
+        return args.alpha == 1.0F ? with_bias(std::false_type{}) : with_bias(std::true_type{});
+    }
     auto with_accumulate = [&](auto with_bias, auto gelu) -> hipError_t {
         if (args.accumulate) {
             return args.alpha == 1.0F ? with_alpha(std::false_type{}, with_bias, gelu, std::true_type{})
@@ -209,16 +244,20 @@ hipError_t gemm_f32(const float* a, const float* b, const float* bias, float* c,
     // 17.8 us, FC1 + GELU 27.9 -> 24.2, projection 10.7 -> 8.4, FC2 25.7 ->
     // 22.7. Wide panels with three wavefronts per SIMD suit the wide outputs,
     // 32-column panels the 192-wide ones.
-    if (args.n >= 512) {
-        if (const hipError_t panel = launch_panel<12, 64, 2, 4, 12>(a, b, bias, c, args, stream);
+    // A batch whose entries share B and whose A rows follow one another (the
+    // patch embedding: 196 rows per image into rows 1.. of its 197) runs as
+    // one problem of all its rows (ViT-Tiny b32 embedding 27 -> 21 us).
+    const GemmArgs whole = as_one_problem(args);
+    if (whole.n >= 512) {
+        if (const hipError_t panel = launch_panel<12, 64, 2, 4, 12>(a, b, bias, c, whole, stream);
             panel != hipErrorNotSupported) {
             return panel;
         }
-    } else if (const hipError_t panel = launch_panel<12, 32, 2, 4, 8>(a, b, bias, c, args, stream);
+    } else if (const hipError_t panel = launch_panel<12, 32, 2, 4, 8>(a, b, bias, c, whole, stream);
                panel != hipErrorNotSupported) {
         return panel;
     }
-    if (const hipError_t panel = launch_panel<48, 32, 2, 4, 12>(a, b, bias, c, args, stream);
+    if (const hipError_t panel = launch_panel<48, 32, 2, 4, 12>(a, b, bias, c, whole, stream);
         panel != hipErrorNotSupported) {
         return panel;
     }
@@ -303,14 +342,7 @@ hipError_t gemm_bf16(const std::uint16_t* a, const std::uint16_t* b, const float
     // runs as one problem of all the rows, so tiles do not stop at entry
     // boundaries (ViT-Base b64 embedding 53 -> 41 us).
     const std::int64_t units = compute_units();
-    GemmArgs whole = args;
-    if (args.count > 1 && args.inner == 0 && args.stride_b == 0 &&
-        args.stride_a == static_cast<std::int64_t>(args.m) * args.lda &&
-        static_cast<std::int64_t>(args.m) * args.count <= 0x7FFFFFFF) {
-        whole.m = args.m * args.count;
-        whole.count = 1;
-        whole.rows_per_entry = args.m;
-    }
+    const GemmArgs whole = as_one_problem(args);
     if (whole.transposed && whole.k >= 512 && tile_count(whole, 256, 192) <= units &&
         tile_count(whole, 128, 128) > 2 * units) {
         using S = Shape<std::uint16_t, 4, 3, 2, 2, 64>;

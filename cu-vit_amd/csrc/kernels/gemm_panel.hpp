@@ -56,8 +56,11 @@ template <int KB, int BN, int TN, int KG, int W> struct PanelShape {
 };
 
 /// @p groups row-tile ranges per panel: workgroup x computes panel x / groups
-/// over range x % groups. The epilogue's parts are compile-time; there is no
-/// addend, and kAlpha false means alpha is 1 (1 * x is x, bit for bit).
+/// over range x % groups. The epilogue's parts are compile-time (kAddend: the
+/// [m, n] addend after the bias, the model's positional add), and kAlpha
+/// false means alpha is 1 (1 * x is x, bit for bit). With
+/// args.rows_per_entry > 0 the rows are batch entries run as one problem:
+/// row p is stored as row p % rows_per_entry of entry p / rows_per_entry.
 ///
 /// Work split. A workgroup's R row tiles make U = R * kParts full items
 /// (16 x 16 TN). The first 4 floor(U / 4) go round robin to the four SIMDs,
@@ -67,7 +70,8 @@ template <int KB, int BN, int TN, int KG, int W> struct PanelShape {
 /// length. The wavefronts of a SIMD take its items in turn; wavefronts w and
 /// w + 4 share a SIMD (the CU places a workgroup's wavefronts on its SIMDs
 /// in turn, read from the hardware id register on MI355X).
-template <int KB, int BN, int TN, int KG, int W, bool kAlpha, bool kBias, bool kGelu, bool kAccumulate>
+template <int KB, int BN, int TN, int KG, int W, bool kAlpha, bool kBias, bool kGelu, bool kAccumulate,
+          bool kAddend = false>
 __global__ __launch_bounds__(kWave * W) void gemm_panel_kernel(const float* __restrict__ a,
                                                              const float* __restrict__ b,
                                                              const float* __restrict__ bias,
@@ -173,10 +177,25 @@ __global__ __launch_bounds__(kWave * W) void gemm_panel_kernel(const float* __re
     // A lane with nothing to store (row past M, columns past N) stores to an
     // offset the buffer resource drops, so the epilogue has no branch.
     const auto c_resource = buffer_resource(c);
-    auto c_offset = [&](int row, int column) {
-        return row < args.m && column < args.n ? static_cast<unsigned int>((row * args.ldc + column) * 4)
+    // Row @p row's place: its element offset in C and its row of the addend
+    // (the entry's own row when entries run as one problem).
+    struct Place {
+        int c_row;
+        int local;
+    };
+    auto place = [&](int row) -> Place {
+        if (args.rows_per_entry > 0) {
+            const int entry = row / args.rows_per_entry;
+            const int local = row - entry * args.rows_per_entry;
+            return {static_cast<int>(entry * args.stride_c) + local * args.ldc, local};
+        }
+        return {row * args.ldc, row};
+    };
+    auto c_offset = [&](int row, const Place& at, int column) {
+        return row < args.m && column < args.n ? static_cast<unsigned int>((at.c_row + column) * 4)
                                                : kOutside;
     };
+    const auto addend_resource = buffer_resource(kAddend ? args.addend : c);
 
     floatx4 acc[TN];
     floatx4 old[TN];
@@ -216,14 +235,16 @@ __global__ __launch_bounds__(kWave * W) void gemm_panel_kernel(const float* __re
 
     auto load_old = [&](auto tiles, int row, int column) {
         constexpr int Tiles = decltype(tiles)::value;
+        const Place at = place(row);
 #pragma unroll
         for (int j = 0; j < Tiles; ++j)
             old[j] = __builtin_bit_cast(
-                floatx4, buffer_load16(c_resource, c_offset(row, col0 + column + 16 * j + 4 * fragment_chunk)));
+                floatx4, buffer_load16(c_resource, c_offset(row, at, col0 + column + 16 * j + 4 * fragment_chunk)));
     };
 
     auto finish = [&](auto tiles, int row, int column) {
         constexpr int Tiles = decltype(tiles)::value;
+        const Place at = place(row);
 #pragma unroll
         for (int j = 0; j < Tiles; ++j) {
             const int within = column + 16 * j + 4 * fragment_chunk;
@@ -231,11 +252,21 @@ __global__ __launch_bounds__(kWave * W) void gemm_panel_kernel(const float* __re
             if constexpr (kBias) {
                 bias_value = __builtin_bit_cast(floatx4, load16(panel_bias + within));
             }
+            floatx4 addend_value{0.F, 0.F, 0.F, 0.F};
+            if constexpr (kAddend) {
+                const int column_index = col0 + within;
+                addend_value = __builtin_bit_cast(
+                    floatx4, buffer_load16(addend_resource,
+                                           row < args.m && column_index < args.n
+                                               ? static_cast<unsigned int>(
+                                                     (at.local * args.ld_addend + column_index) * 4)
+                                               : kOutside));
+            }
             floatx4 value;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 // epilogue_value's steps with its flags fixed: alpha, the
-                // bias, GELU, each rounded on its own.
+                // bias, the addend, GELU, each rounded on its own.
 #pragma clang fp contract(off)
                 float v = acc[j][r];
                 if constexpr (kAlpha) {
@@ -243,6 +274,9 @@ __global__ __launch_bounds__(kWave * W) void gemm_panel_kernel(const float* __re
                 }
                 if constexpr (kBias) {
                     v += bias_value[r];
+                }
+                if constexpr (kAddend) {
+                    v += addend_value[r];
                 }
                 if constexpr (kGelu) {
                     v = gelu(v);
@@ -255,7 +289,7 @@ __global__ __launch_bounds__(kWave * W) void gemm_panel_kernel(const float* __re
                     value[r] = add_unfused(old[j][r], value[r]);
             }
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, value), c_resource,
-                                                   c_offset(row, col0 + within), 0, 0);
+                                                   c_offset(row, at, col0 + within), 0, 0);
         }
     };
 

@@ -80,3 +80,29 @@ def test_panel_equals_the_tiled_kernel(cuvit, oracle, device, m, n, k, with_bias
                              1.0e-6, 1.0e-5)
     padding = to_host(c).reshape(m, ldc)[:, n:]
     require_exact(padding, start_c.reshape(m, ldc)[:, n:], "the columns past N changed")
+
+
+def test_panel_runs_a_shared_weight_batch_as_one_problem(cuvit, oracle, device):
+    """A batch of 32 entries of 196 rows with B shared and A rows following one
+    another (the ViT-Tiny patch embedding's shape, 6272 x 192 x 768) runs as
+    one problem on the panel kernel; each entry lands at its own C stride (197
+    rows apart, so one row per entry is never written) and equals its own
+    launch of 196 rows, bit for bit."""
+    entries, m, n, k = 32, 196, 192, 768
+    g = oracle.generator(4242)
+    a = g.normal(entries * m * k)
+    w = g.normal(n * k, 0.0, 0.05)
+    bias = to_device(g.normal(n, 0.0, 0.5), device)
+    start = g.normal(entries * (m + 1) * n)
+    da, dw = to_device(a, device), to_device(w, device)
+    p = cuvit.gemm_problem(m, n, k, cuvit.TRANSPOSED)
+    p.batch.count, p.batch.stride_a, p.batch.stride_b, p.batch.stride_c = entries, m * k, 0, (m + 1) * n
+    c = to_device(start, device)
+    cuvit.gemm(da, dw, bias, c, p)
+    full = to_host(c).reshape(entries, m + 1, n)
+    require_exact(full[:, m], start.reshape(entries, m + 1, n)[:, m], "the rows between entries changed")
+    single = cuvit.gemm_problem(m, n, k, cuvit.TRANSPOSED)
+    one = torch.full((m * n,), float("nan"), device=device)
+    for entry in (0, 1, 17, 31):
+        cuvit.gemm(da[entry * m * k:], dw, bias, one, single)
+        require_exact(to_host(one).reshape(m, n), full[entry, :m], f"batch entry {entry}")
