@@ -1,15 +1,18 @@
-// Host dispatch of the batched GEMM (the kernel is in gemm_kernel.hpp).
-//
-// Two workgroup tiles per type, measured on MI355X at the ViT shapes:
-//   fp32 (16 x 16 MFMA): 32 x 32 for every ViT-Tiny GEMM (at batch 32, FC2
-//        6304 x 192 x 768 in 25 us against 34 us for 64 x 64, FC1 6304 x 768
-//        x 192 in 28 us, attention 197 x 197 x 64 in 3.7 us); 64 x 64 once
-//        a problem has work for more than 32 small tiles per compute unit.
-//   bf16 (32 x 32 MFMA): 128 x 128 once a problem fills every compute unit
-//        twice with it (ViT-Base FC2 12608 x 768 x 3072: 118 us against
-//        130 us for 64 x 64), else 64 x 64; 128 x 128 with 32-deep stages
-//        up to K = 1024.
-// Both tiles of a type run the same MFMA over K in the same order, so the
+// Host dispatch of the batched GEMM. The kernels, all measured on MI355X at
+// the ViT shapes and picked in this order:
+//   fp32 (16 x 16 MFMA): the resident-panel kernel (gemm_panel.hpp) for
+//        tall products with B as [N, K] and K of 192 or 768 (the ViT-Tiny
+//        linear layers and patch embedding); else the tiled kernel
+//        (gemm_kernel.hpp), 32 x 32 tiles, 64 x 64 once a problem has work
+//        for more than 32 small tiles per compute unit.
+//   bf16 (32 x 32 MFMA): the wide kernel (gemm_wide.hpp, 128 x 256 tiles)
+//        for large products without accumulation (ViT-Base FC1, QKV); the
+//        tiled kernel's twelve-wavefront 256 x 192 tile when one round of it
+//        covers a product that 128 x 128 tiles would need more than two per
+//        compute unit for (ViT-Base FC2, projection, patch embedding); else
+//        128 x 128 once a problem fills every compute unit twice with it
+//        (32-deep stages up to K = 1024), else 64 x 64.
+// Every kernel of a type runs the same MFMA over K in the same order, so the
 // choice never changes a result.
 #include "gemm_kernel.hpp"
 #include "gemm_panel.hpp"
