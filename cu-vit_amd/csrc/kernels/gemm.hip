@@ -249,7 +249,7 @@ hipError_t gemm_f32(const float* a, const float* b, const float* bias, float* c,
     // 32-column panels the 192-wide ones.
     // A batch whose entries share B and whose A rows follow one another (the
     // patch embedding: 196 rows per image into rows 1.. of its 197) runs as
-    // one problem of all its rows (ViT-Tiny b32 embedding 27 -> 21 us).
+    // one problem of all its rows (ViT-Tiny b32 embedding 27 -> 22 us).
     const GemmArgs whole = as_one_problem(args);
     if (whole.n >= 512) {
         if (const hipError_t panel = launch_panel<12, 64, 2, 4, 12>(a, b, bias, c, whole, stream);
