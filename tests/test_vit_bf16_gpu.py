@@ -204,3 +204,36 @@ def test_bf16_weight_file_loads_to_the_same_models(cuvit, oracle, device, tmp_pa
                   "bf16 model: bf16 file vs fp32 file")
     require_exact(logits(mixed, cuvit.PRECISION_F32), logits(widened_path, cuvit.PRECISION_F32),
                   "fp32 model: bf16 file vs widened fp32 file")
+
+
+def test_bf16_vit_base_batch_64_sequence(cuvit, oracle, device, tmp_path):
+    """ViT-Base/16 widths (768, 12 heads, MLP 3072) with two blocks, batch 64,
+    N(0, 0.02) weights: the C5 kernels at their production shapes (the wide
+    GEMM for QKV and FC1, the twelve-wavefront tile for FC2, the projection
+    and the patch embedding run as one problem with its positional addend,
+    the persistent attention over 768 (image, head) pairs, the class-row final
+    LayerNorm). Image 0 is held to the bf16 tolerance against both oracles,
+    and images of the batch are bitwise equal to the same images run alone
+    (small tiles there)."""
+    config = tiny_config(cuvit)
+    config.embed_dim, config.depth, config.heads, config.mlp_hidden = 768, 2, 12, 3072
+    tensors = random_weights(cuvit, oracle, config, 505, small=False)
+    path = os.path.join(tmp_path, "base.cvw")
+    write_weights(cuvit, tensors, path)
+    weights = cuvit.WeightFile(path)
+    batch = 64
+    images = [random_image(oracle, config, 900 + i) for i in range(batch)]
+    model = cuvit.VisionTransformer(config, weights, batch, cuvit.PRECISION_BF16)
+    together = forward(model, np.concatenate(images), batch, device)
+    assert np.isfinite(together).all()
+    values = [t for _, t in tensors]
+    reduced = relative_l2(together[0], oracle.vit_forward(config, values, images[0], bf16=True))
+    full = relative_l2(together[0], oracle.vit_forward(config, values, images[0]))
+    print(f"image 0: vs bf16 oracle {reduced:.2e}, vs fp32 oracle {full:.2e}")
+    if reduced > TINY_L2 or full > TINY_L2:
+        raise TestFailure(f"bf16 ViT-Base: relative L2 {reduced:.3e} against the bf16 oracle, "
+                          f"{full:.3e} against the fp32 oracle")
+    single = cuvit.VisionTransformer(config, weights, 1, cuvit.PRECISION_BF16)
+    for i in (0, 37, 63):
+        alone = forward(single, images[i], 1, device)[0]
+        require_exact(together[i], alone, f"bf16 ViT-Base image {i} of the batch differs from it alone")
