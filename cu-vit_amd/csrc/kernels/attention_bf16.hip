@@ -196,13 +196,32 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
         std::uint16_t* const values = lds + buffer * kBufferElements;
         std::uint16_t* const keys = values + kPadded * kHeadDim;
         const auto resource = gemm::buffer_resource(b.k);
-        for (int c = threadIdx.x; c < kPadded * kChunks; c += blockDim.x) {
-            const int key = c / kChunks;
-            const int d0 = 8 * (c % kChunks);
-            const Vec16 v = load_or_zero(resource, key * qkv_row + d0 + embed, key < tokens);
-            const Vec16 k = load_or_zero(resource, key * qkv_row + d0, key < tokens);
-            store16(values + value_slot(key, d0), v);
-            store16(keys + key * kKeyPitch + d0, k);
+        // Rounds of kRound chunks per thread: a round's loads all go out
+        // before its stores, one latency per round.
+        constexpr int kRound = 4;
+        const int threads = static_cast<int>(blockDim.x);
+        for (int c0 = threadIdx.x; c0 < kPadded * kChunks; c0 += kRound * threads) {
+            Vec16 v[kRound];
+            Vec16 k[kRound];
+#pragma unroll
+            for (int r = 0; r < kRound; ++r) {
+                const int c = c0 + r * threads;
+                const int key = c / kChunks;
+                const int d0 = 8 * (c % kChunks);
+                const bool inside = c < kPadded * kChunks && key < tokens;
+                v[r] = load_or_zero(resource, key * qkv_row + d0 + embed, inside);
+                k[r] = load_or_zero(resource, key * qkv_row + d0, inside);
+            }
+#pragma unroll
+            for (int r = 0; r < kRound; ++r) {
+                const int c = c0 + r * threads;
+                if (c < kPadded * kChunks) {
+                    const int key = c / kChunks;
+                    const int d0 = 8 * (c % kChunks);
+                    store16(values + value_slot(key, d0), v[r]);
+                    store16(keys + key * kKeyPitch + d0, k[r]);
+                }
+            }
         }
     };
     // The same through registers: chunk c of the pair's 2 * kPadded * 8 is
@@ -259,8 +278,16 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
     int buffer = 0;
     Vec16 q[kHeadDim / kKBlock];
     Vec16 q_ahead[kHeadDim / kKBlock];
-    load_direct(pair_bases(qkv, pair, heads, tokens), 0);
+    // The first pair: its Q, then (with a prefetch register set) all of its
+    // K and V loads in flight before the first LDS store, one latency in all
+    // (the strided loop below waits for each round of loads in turn).
     load_queries(pair_bases(qkv, pair, heads, tokens), q);
+    if constexpr (Chunks > 0) {
+        prefetch(pair_bases(qkv, pair, heads, tokens));
+        commit(0);
+    } else {
+        load_direct(pair_bases(qkv, pair, heads, tokens), 0);
+    }
     __syncthreads();
     for (;;) {
     const int next = pair + static_cast<int>(gridDim.y);
