@@ -19,9 +19,10 @@
 // an accumulator starting at +0. So the two kernels give bitwise the same C,
 // and which one runs depends on the shape only.
 //
-// Epilogue. alpha, the bias and GELU are applied in registers (the bias for
-// the lane's 64 columns loaded after the k loop; the flags, and whether alpha
-// differs from 1, as template parameters: 1 * x is x, bit for bit), each
+// Epilogue. alpha, the bias and GELU are applied in registers (the tile's
+// bias staged into LDS before the k loop, read from there; the flags, and
+// whether alpha differs from 1, as template parameters: 1 * x is x, bit for
+// bit), each
 // value rounded once to bf16 and written into the LDS as a [BM][BN] tile with
 // 16-byte chunk c of row r at c ^ (r % chunks_per_row); after a barrier each
 // wavefront reads whole rows back and stores them with 16-byte non-temporal
@@ -50,7 +51,9 @@ template <int TM, int TN> struct WideShape {
     static constexpr int kStageChunks = (kBM + kBN) * kRowChunks;
     static constexpr std::size_t kStageBytes = 2 * static_cast<std::size_t>(kStageChunks) * 16;
     static constexpr std::size_t kTileBytes = static_cast<std::size_t>(kBM) * kBN * 2;
-    static constexpr std::size_t kLdsBytes = kStageBytes > kTileBytes ? kStageBytes : kTileBytes;
+    static constexpr std::size_t kCoreBytes = kStageBytes > kTileBytes ? kStageBytes : kTileBytes;
+    /// The stages or the C tile, then the tile's bias (kBN floats).
+    static constexpr std::size_t kLdsBytes = kCoreBytes + static_cast<std::size_t>(kBN) * 4;
     static_assert(kBM * kRowChunks % kThreads == 0 && kBN * kRowChunks % kThreads == 0,
                   "whole stage chunks per thread");
 
@@ -104,6 +107,22 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_wide_kernel(const std::uint1
     const int col0 = tile_n * BN;
     const int steps = (args.k + kSpan<std::uint16_t> - 1) / kSpan<std::uint16_t> *
                       (kSpan<std::uint16_t> / S::kBK);
+
+    // The tile's bias into LDS once, ahead of every k loop, columns past N
+    // reading as zero: the epilogue then reads it from LDS instead of waiting
+    // on global loads after the k loop.
+    float* const tile_bias = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(lds_vectors) +
+                                                      S::kCoreBytes);
+    if constexpr (kBias) {
+        if (threadIdx.x < BN / 4) {
+            const int col = col0 + 4 * static_cast<int>(threadIdx.x);
+            // N is a multiple of 8 here, so a run of four starts and ends inside
+            const Vec16 v = buffer_load16(buffer_resource(bias),
+                                          col < args.n ? static_cast<unsigned int>(col) * 4U : kOutside);
+            store16(tile_bias + 4 * threadIdx.x, v);
+        }
+        __syncthreads();
+    }
 
     for (int entry = blockIdx.y; entry < args.count; entry += gridDim.y) {
         const Offsets off = entry_offsets(args, entry);
@@ -198,20 +217,17 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_wide_kernel(const std::uint1
 
         // Epilogue through LDS: the k loop ended on a barrier, so the stage
         // buffers are free. The bias of the lane's 64 columns (tile j, run q
-        // of four columns) comes in 16 buffer loads of 16 bytes, all in
-        // flight together, columns past N reading as zero (held over the k
-        // loop it would cost the registers of a second workgroup).
+        // of four columns) comes from the tile's bias in LDS (held in
+        // registers over the k loop it would cost the registers of a second
+        // workgroup).
         float column_bias[TN][4][4];
         if constexpr (kBias) {
-            const auto bias_resource = buffer_resource(bias);
 #pragma unroll
             for (int j = 0; j < TN; ++j)
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const int col = col0 + wave_n * TN * E + j * E + Mma<std::uint16_t>::column(lane, q);
-                    // N is a multiple of 8 here, so a run of four starts and ends inside
-                    const Vec16 v = buffer_load16(
-                        bias_resource, col < args.n ? static_cast<unsigned int>(col) * 4U : kOutside);
+                    const Vec16 v =
+                        load16(tile_bias + wave_n * TN * E + j * E + Mma<std::uint16_t>::column(lane, q));
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         column_bias[j][q][e] = __uint_as_float(v.w[e]);
