@@ -132,12 +132,6 @@ __device__ __forceinline__ float epilogue_value(float sum, bool with_bias, float
     return value;
 }
 
-__device__ __forceinline__ float epilogue_value(float sum, const float* bias, int row, int column,
-                                                const GemmArgs& args) {
-    return epilogue_value(sum, bias != nullptr, bias != nullptr ? bias[column] : 0.0F, row, column,
-                          args);
-}
-
 // -- operand loads ------------------------------------------------------------
 //
 // The vector path reads operands with raw buffer loads. A buffer resource
@@ -200,12 +194,22 @@ __device__ __forceinline__ float add_unfused(float c, float value) {
     return c + value;
 }
 
-/// Stores four consecutive results (C = value, or C += value), 16 bytes for
-/// fp32 and 8 for bf16; @p p is aligned to that size.
-__device__ __forceinline__ void store4(float* p, const float (&value)[4], bool accumulate) {
+/// Four consecutive elements of C as one load: 16 bytes for fp32, 8 for bf16.
+template <typename T> struct Quad;
+template <> struct Quad<float> {
+    using Type = floatx4;
+};
+template <> struct Quad<std::uint16_t> {
+    using Type = uint2;
+};
+
+/// Stores four consecutive results (C = value, or C = @p old + value when
+/// accumulating, @p old being the four elements read beforehand); @p p is
+/// aligned to the four elements' size.
+__device__ __forceinline__ void store4(float* p, const float (&value)[4], bool accumulate,
+                                       const floatx4& old) {
     floatx4 v{value[0], value[1], value[2], value[3]};
     if (accumulate) {
-        const floatx4 old = *reinterpret_cast<const floatx4*>(p);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             v[r] = add_unfused(old[r], v[r]);
@@ -213,10 +217,10 @@ __device__ __forceinline__ void store4(float* p, const float (&value)[4], bool a
     *reinterpret_cast<floatx4*>(p) = v;
 }
 
-__device__ __forceinline__ void store4(std::uint16_t* p, const float (&value)[4], bool accumulate) {
+__device__ __forceinline__ void store4(std::uint16_t* p, const float (&value)[4], bool accumulate,
+                                       const uint2& old) {
     float v[4] = {value[0], value[1], value[2], value[3]};
     if (accumulate) {
-        const uint2 old = *reinterpret_cast<const uint2*>(p);
         v[0] = add_unfused(bf16_to_float(static_cast<std::uint16_t>(old.x & 0xFFFFU)), v[0]);
         v[1] = add_unfused(bf16_to_float(static_cast<std::uint16_t>(old.x >> 16)), v[1]);
         v[2] = add_unfused(bf16_to_float(static_cast<std::uint16_t>(old.y & 0xFFFFU)), v[2]);
@@ -545,7 +549,28 @@ __global__ __launch_bounds__(kWave * WM * WN) __attribute__((amdgpu_waves_per_eu
         }
 
         // Epilogue: lane holds row fragment_row of each MFMA tile in runs of
-        // four consecutive columns.
+        // four consecutive columns. The bias of each whole run (inside N) is
+        // read once for all the tile's rows, all runs' loads in flight
+        // together; a run that N cuts reads its bias element by element.
+        float run_bias[TN][Mma<T>::kRuns][4] = {};
+        if (bias != nullptr) {
+            // The resource ends at N: a run past N reads zeros, with no select
+            // on the offset (a run that N cuts is not read from here).
+            const auto bias_resource = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(bias), static_cast<short>(0), args.n * 4, 0x00020000);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+#pragma unroll
+                for (int q = 0; q < Mma<T>::kRuns; ++q) {
+                    const int col = col0 + wave_n * TN * E + j * E + Mma<T>::column(lane, q);
+                    const Vec16 v = buffer_load16(bias_resource, static_cast<unsigned int>(col) * 4U);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        run_bias[j][q][r] = __uint_as_float(v.w[r]);
+                    }
+                }
+            }
+        }
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             const int row = row0 + wave_m * TM * E + i * E + fragment_row;
@@ -561,6 +586,23 @@ __global__ __launch_bounds__(kWave * WM * WN) __attribute__((amdgpu_waves_per_eu
                 c_offset = entry_index * args.stride_c + static_cast<std::int64_t>(local) * args.ldc;
             }
             T* const c_row = c_entry + c_offset;
+            // C may alias nothing the kernel reads, but the compiler cannot
+            // know it: read the row's old values for all runs before the
+            // first store, so the loads overlap instead of each waiting
+            // behind the store before it.
+            typename Quad<T>::Type old[TN][Mma<T>::kRuns] = {};
+            if (vector_c && args.accumulate) {
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+#pragma unroll
+                    for (int q = 0; q < Mma<T>::kRuns; ++q) {
+                        const int col = col0 + wave_n * TN * E + j * E + Mma<T>::column(lane, q);
+                        if (col + 3 < args.n) {
+                            old[j][q] = *reinterpret_cast<const typename Quad<T>::Type*>(c_row + col);
+                        }
+                    }
+                }
+            }
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
 #pragma unroll
@@ -569,15 +611,20 @@ __global__ __launch_bounds__(kWave * WM * WN) __attribute__((amdgpu_waves_per_eu
                     if (col >= args.n) {
                         continue;
                     }
+                    const bool whole_run = col + 3 < args.n;
                     float value[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        value[r] = col + r < args.n
-                                       ? epilogue_value(acc[i][j][4 * q + r], bias, local, col + r, args)
-                                       : 0.F;
+                        value[r] = 0.F;
+                        if (col + r < args.n) {
+                            const float bias_value =
+                                bias == nullptr ? 0.F : whole_run ? run_bias[j][q][r] : bias[col + r];
+                            value[r] = epilogue_value(acc[i][j][4 * q + r], bias != nullptr, bias_value,
+                                                      local, col + r, args);
+                        }
                     }
-                    if (vector_c && col + 3 < args.n) {
-                        store4(c_row + col, value, args.accumulate);
+                    if (vector_c && whole_run) {
+                        store4(c_row + col, value, args.accumulate, old[j][q]);
                     } else {
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
