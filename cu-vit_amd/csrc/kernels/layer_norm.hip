@@ -105,26 +105,62 @@ __global__ __launch_bounds__(kBlock) void layer_norm_vector_kernel(
         }
     }
 
+    // Rows too wide for that at a fixed width (bf16 at 768: 48 columns a
+    // lane) take gamma and beta from LDS, staged once per workgroup. Their
+    // loads are issued right behind the first row's, so the two round trips
+    // overlap instead of the parameters' following the row statistics.
+    constexpr bool kStage = !kHoist && kColumns > 0;
+    constexpr int kParamQuads = kStage ? 2 * kColumns / 4 : 1;  // gamma's float4s, then beta's
+    __shared__ float4 staged_params[kParamQuads];
+
     const float inverse_columns = 1.0F / static_cast<float>(columns);
     const std::int64_t groups = (static_cast<std::int64_t>(rows) + kTeams - 1) / kTeams;
     const std::int64_t wave_count = static_cast<std::int64_t>(gridDim.x) * kWavesPerBlock;
     const std::int64_t first_wave =
         static_cast<std::int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
 
-    for (std::int64_t group = first_wave; group < groups; group += wave_count) {
+    // A group's rows into registers (zeros past the last row); the next
+    // group's are read at the end of the current one.
+    Vec16 raw[V];
+    auto load_group = [&](std::int64_t group) {
         const std::int64_t row = group * kTeams + team;
-        const bool row_valid = row < rows;
         const T* const source = input + row * (Strided ? input_stride : columns);
-
-        Vec16 raw[V];
 #pragma unroll
         for (int j = 0; j < V; ++j) {
             raw[j] = Vec16{{0U, 0U, 0U, 0U}};
-            if (row_valid && valid[j]) {
+            if (row < rows && valid[j]) {
                 raw[j] = Streaming ? load16_streaming(source + (team_lane + Lanes * j) * E)
                                    : load16(source + (team_lane + Lanes * j) * E);
             }
         }
+    };
+    load_group(first_wave);
+    if constexpr (kStage) {
+        // Thread t holds quads t and t + kBlock (two named registers: an
+        // array here is placed in LDS by the compiler).
+        static_assert(kParamQuads > kBlock && kParamQuads <= 2 * kBlock,
+                      "gamma and beta in two rounds, the first whole");
+        auto param = [&](int index) {
+            return index < kColumns / 4 ? reinterpret_cast<const float4*>(gamma)[index]
+                                        : reinterpret_cast<const float4*>(beta)[index - kColumns / 4];
+        };
+        const int first = static_cast<int>(threadIdx.x);
+        const int second = first + kBlock;
+        const float4 first_quad = param(first);
+        float4 second_quad = make_float4(0.F, 0.F, 0.F, 0.F);
+        if (second < kParamQuads) {
+            second_quad = param(second);
+        }
+        staged_params[first] = first_quad;
+        if (second < kParamQuads) {
+            staged_params[second] = second_quad;
+        }
+        __syncthreads();
+    }
+
+    for (std::int64_t group = first_wave; group < groups; group += wave_count) {
+        const std::int64_t row = group * kTeams + team;
+        const bool row_valid = row < rows;
 
         // x0 lives in element 0 of the team's first lane.
         const float x0 =
@@ -171,8 +207,15 @@ __global__ __launch_bounds__(kBlock) void layer_norm_vector_kernel(
                                 bv[i] = b[j][e + i];
                             }
                         } else {
-                            const float4 gq = *reinterpret_cast<const float4*>(gamma + column + e);
-                            const float4 bq = *reinterpret_cast<const float4*>(beta + column + e);
+                            float4 gq;
+                            float4 bq;
+                            if constexpr (kStage) {
+                                gq = staged_params[(column + e) / 4];
+                                bq = staged_params[kColumns / 4 + (column + e) / 4];
+                            } else {
+                                gq = *reinterpret_cast<const float4*>(gamma + column + e);
+                                bq = *reinterpret_cast<const float4*>(beta + column + e);
+                            }
                             gv[0] = gq.x; gv[1] = gq.y; gv[2] = gq.z; gv[3] = gq.w;
                             bv[0] = bq.x; bv[1] = bq.y; bv[2] = bq.z; bv[3] = bq.w;
                         }
@@ -188,6 +231,9 @@ __global__ __launch_bounds__(kBlock) void layer_norm_vector_kernel(
                     }
                 }
             }
+        }
+        if (group + wave_count < groups) {
+            load_group(group + wave_count);
         }
     }
 }

@@ -27,7 +27,10 @@ def bf16_inputs(oracle, seed, count, mean=0.0, stddev=1.0):
 
 
 @pytest.mark.parametrize("rows,columns", [(12608, 768), (197, 768), (1, 192), (6304, 192),
-                                          (5, 31), (3, 1), (7, 2056)])
+                                          (5, 31), (3, 1), (7, 2056),
+                                          # more row groups than wavefronts: each
+                                          # wavefront reads its next group ahead
+                                          (40003, 768)])
 def test_layer_norm_bf16(cuvit, oracle, device, rows, columns):
     bits, values = bf16_inputs(oracle, 505 + rows + columns, rows * columns)
     g = oracle.generator(506)

@@ -91,7 +91,9 @@ def test_residual_add_sizes(cuvit, oracle, device, count, offset):
 
 LN_SHAPES = [(1, 192), (197, 192), (197, 768), (3, 1), (5, 31), (2, 1024),
              # beyond the reference: ViT-Tiny batch 32, ViT-Base rows, odd widths
-             (6304, 192), (64, 768), (7, 4), (9, 36), (11, 2048), (4, 4100)]
+             (6304, 192), (64, 768), (7, 4), (9, 36), (11, 2048), (4, 4100),
+             # more row groups than wavefronts (grid-stride loop)
+             (70001, 192)]
 
 
 @pytest.mark.parametrize("rows,columns", LN_SHAPES)
