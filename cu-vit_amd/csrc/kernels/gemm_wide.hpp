@@ -266,16 +266,28 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_wide_kernel(const std::uint1
         }
         __syncthreads();
         constexpr int kRowsPerStore = kWave / kTileChunks;
-#pragma unroll 4
-        for (int it = 0; it < BM / (4 * kRowsPerStore); ++it) {
-            const int r = (it * 4 + wave) * kRowsPerStore + lane / kTileChunks;
-            const int chunk = lane % kTileChunks;
-            const Vec16 v = *reinterpret_cast<const Vec16*>(tile + r * (BN * 2) +
-                                                            ((chunk ^ (r % kTileChunks)) * 16));
-            const int row = row0 + r;
-            const int col = col0 + 8 * chunk;
-            if (row < args.m && col < args.n) {  // N is a multiple of 8 on this path
-                store16_streaming(c_entry + static_cast<std::int64_t>(row) * args.ldc + col, v);
+        constexpr int kStoreRounds = BM / (4 * kRowsPerStore);
+        // Four rounds' LDS reads issued together, then their stores: a read
+        // per store, each waited on before its store, left the LDS latency
+        // exposed sixteen times a tile.
+        constexpr int kBatch = kStoreRounds % 4 == 0 ? 4 : 1;
+        const int chunk = lane % kTileChunks;
+        const int col = col0 + 8 * chunk;
+#pragma unroll 1
+        for (int it0 = 0; it0 < kStoreRounds; it0 += kBatch) {
+            Vec16 v[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const int r = ((it0 + u) * 4 + wave) * kRowsPerStore + lane / kTileChunks;
+                v[u] = *reinterpret_cast<const Vec16*>(tile + r * (BN * 2) +
+                                                       ((chunk ^ (r % kTileChunks)) * 16));
+            }
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const int row = row0 + ((it0 + u) * 4 + wave) * kRowsPerStore + lane / kTileChunks;
+                if (row < args.m && col < args.n) {  // N is a multiple of 8 on this path
+                    store16_streaming(c_entry + static_cast<std::int64_t>(row) * args.ldc + col, v[u]);
+                }
             }
         }
         __syncthreads();  // the next entry refills the LDS
