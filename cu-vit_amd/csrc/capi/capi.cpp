@@ -343,6 +343,18 @@ int gemm_bf16_with_addend(const std::uint16_t* a, const std::uint16_t* b, const 
     return from_hip(detail::gemm_bf16(a, b, bias, c, resolved.args, stream), "gemm launch");
 }
 
+int extract_patches_f32_to_bf16(const float* images, std::uint16_t* patches, int batch,
+                                int channels, int height, int width, int patch,
+                                hipStream_t stream, bool* fused) {
+    const hipError_t result = detail::extract_patches_f32_to_bf16(images, patches, batch, channels,
+                                                                  height, width, patch, stream);
+    *fused = result != hipErrorNotSupported;
+    if (!*fused) {
+        return ok();
+    }
+    return from_hip(result, "extract_patches launch");
+}
+
 int layer_norm_cached(const float* input, const float* gamma, const float* beta, float* output,
                       int rows, int columns, float epsilon, hipStream_t stream,
                       std::int64_t input_stride) {

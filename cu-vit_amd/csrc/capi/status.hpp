@@ -53,6 +53,15 @@ int layer_norm_cached(const std::uint16_t* input, const float* gamma, const floa
                       std::uint16_t* output, int rows, int columns, float epsilon,
                       hipStream_t stream, std::int64_t input_stride = 0);
 
+/// fp32 images into the bf16 model's patch rows in one pass (bitwise the
+/// conversion to bf16 followed by the bf16 gather) when the layout allows it:
+/// 16-byte aligned pointers, patch size and image width multiples of 8.
+/// @p fused tells whether it ran; when it did not, nothing was launched and
+/// the caller converts and gathers.
+int extract_patches_f32_to_bf16(const float* images, std::uint16_t* patches, int batch,
+                                int channels, int height, int width, int patch,
+                                hipStream_t stream, bool* fused);
+
 /// The checks of preprocess (image.cpp:96-104, 126-128), in its order: an
 /// empty image, a non-positive size, a crop fraction outside (0, 1], a zero
 /// standard deviation.

@@ -469,16 +469,26 @@ void VisionTransformer::forward_stored(Stored<T>& stored, const float* images, f
     const int embed = config_.embed_dim;
     const std::int64_t tokens_per_image = static_cast<std::int64_t>(token_count) * embed;
 
-    const T* source = nullptr;
     if constexpr (kFloat) {
-        source = images;
+        launch_extract_patches(images, stored.patches, batch, config_.channels, config_.image_size,
+                               config_.image_size, config_.patch_size, stream);
     } else {
-        throw_on_error(cuvit_convert_f32_to_bf16(
-            images, stored.images, static_cast<std::int64_t>(batch) * image_elements(), as_c(stream)));
-        source = stored.images;
+        // The conversion to bf16 and the gather in one pass where the layout
+        // allows (the same bits: rounding does not depend on the position);
+        // else the images are converted, then gathered.
+        bool fused = false;
+        throw_on_error(capi::extract_patches_f32_to_bf16(
+            images, stored.patches, batch, config_.channels, config_.image_size,
+            config_.image_size, config_.patch_size, stream, &fused));
+        if (!fused) {
+            throw_on_error(cuvit_convert_f32_to_bf16(images, stored.images,
+                                                     static_cast<std::int64_t>(batch) * image_elements(),
+                                                     as_c(stream)));
+            launch_extract_patches(stored.images, stored.patches, batch, config_.channels,
+                                   config_.image_size, config_.image_size, config_.patch_size,
+                                   stream);
+        }
     }
-    launch_extract_patches(source, stored.patches, batch, config_.channels, config_.image_size,
-                           config_.image_size, config_.patch_size, stream);
 
     // Patch embeddings land in rows 1.. of each image, with the positional
     // embedding of those rows added in the GEMM's epilogue after the bias:

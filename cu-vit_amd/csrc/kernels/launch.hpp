@@ -47,6 +47,12 @@ hipError_t softmax_bf16(const std::uint16_t* input, std::uint16_t* output, int r
 // element size (4 for fp32, 2 for bf16).
 hipError_t extract_patches(const void* images, void* patches, int element_size, int batch,
                            int channels, int height, int width, int patch, hipStream_t stream);
+/// fp32 images into bf16 patch rows in one pass (bitwise the conversion then
+/// the bf16 gather); hipErrorNotSupported unless both pointers are 16-byte
+/// aligned and the patch and image widths are multiples of 8.
+hipError_t extract_patches_f32_to_bf16(const float* images, std::uint16_t* patches, int batch,
+                                      int channels, int height, int width, int patch,
+                                      hipStream_t stream);
 hipError_t broadcast_f32(float* destination, const float* source, std::int64_t count,
                          std::int64_t destination_stride, int batch, hipStream_t stream);
 hipError_t broadcast_bf16(std::uint16_t* destination, const std::uint16_t* source,

@@ -104,6 +104,74 @@ __global__ __launch_bounds__(kBlock) void extract_patches_strip_kernel(
     }
 }
 
+/// The bf16 model's first step in one pass: fp32 images gathered into bf16
+/// patch rows, each value rounded once to nearest-even (float_to_bf16's
+/// rounding, as the conversion kernel does). A value's rounding does not
+/// depend on where it moves, so the result is bitwise the conversion followed
+/// by the bf16 strip gather, without the bf16 image written and read back.
+/// A unit is 8 elements: 32 bytes read (two 16-byte loads), 16 written.
+/// @tparam PV 16-byte output vectors per patch row (P = 8 PV).
+template <int PV>
+__global__ __launch_bounds__(kBlock) void extract_patches_strip_f32_to_bf16_kernel(
+    const float* __restrict__ images, std::uint16_t* __restrict__ patches, int channels,
+    int height, int width, std::int64_t strips) {
+    constexpr int kVec = 8;
+    constexpr int kPatch = PV * kVec;
+    constexpr int kChunkVectors = kPatch * PV;
+
+    const int patches_across = width / kPatch;
+    const int patches_down = height / kPatch;
+    const int strip_vectors = patches_across * kChunkVectors;
+    const std::int64_t row_elements = static_cast<std::int64_t>(channels) * kPatch * kPatch;
+
+    for (std::int64_t strip = blockIdx.x; strip < strips; strip += gridDim.x) {
+        const std::int64_t plane = strip / patches_down; // image * channels + channel
+        const int patch_row = static_cast<int>(strip - plane * patches_down);
+        const std::int64_t image = plane / channels;
+        const int channel = static_cast<int>(plane - image * channels);
+
+        const float* const source =
+            images + (plane * height + static_cast<std::int64_t>(patch_row) * kPatch) * width;
+        const std::int64_t first_patch =
+            (image * patches_down + patch_row) * static_cast<std::int64_t>(patches_across);
+        std::uint16_t* const destination =
+            patches + first_patch * row_elements + static_cast<std::int64_t>(channel) * kPatch * kPatch;
+
+        for (int first = threadIdx.x; first < strip_vectors; first += kBlock * kUnroll) {
+            Vec16 low[kUnroll];
+            Vec16 high[kUnroll];
+            std::int64_t destination_element[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const int v = first + u * kBlock;
+                const int patch_column = v / kChunkVectors; // power-of-two divisor
+                const int q = v % kChunkVectors;
+                const int local_row = q / PV;
+                const int local_vector = q % PV;
+                const std::int64_t source_element =
+                    static_cast<std::int64_t>(local_row) * width + patch_column * kPatch +
+                    local_vector * kVec;
+                destination_element[u] = static_cast<std::int64_t>(patch_column) * row_elements +
+                                         static_cast<std::int64_t>(q) * kVec;
+                if (v < strip_vectors) {
+                    low[u] = load16(source + source_element);
+                    high[u] = load16(source + source_element + 4);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                if (first + u * kBlock < strip_vectors) {
+                    const Vec16 packed{{pack_bf16x2(__uint_as_float(low[u].w[0]), __uint_as_float(low[u].w[1])),
+                                        pack_bf16x2(__uint_as_float(low[u].w[2]), __uint_as_float(low[u].w[3])),
+                                        pack_bf16x2(__uint_as_float(high[u].w[0]), __uint_as_float(high[u].w[1])),
+                                        pack_bf16x2(__uint_as_float(high[u].w[2]), __uint_as_float(high[u].w[3]))}};
+                    store16_streaming(destination + destination_element[u], packed);
+                }
+            }
+        }
+    }
+}
+
 /// Pair kernel: fp32, three channels, 16 x 16 patches, an even number of patch
 /// columns (ViT/16 at 224). One wavefront per task, a task being (image, patch
 /// row, pair of adjacent patch columns). The task's source is 48 row units
@@ -371,6 +439,27 @@ hipError_t dispatch_patches(const void* images, void* patches, int batch, int ch
 }
 
 } // namespace
+
+hipError_t extract_patches_f32_to_bf16(const float* images, std::uint16_t* patches, int batch,
+                                      int channels, int height, int width, int patch,
+                                      hipStream_t stream) {
+    if (!aligned16(images) || !aligned16(patches) || patch % 8 != 0 || width % 8 != 0) {
+        return hipErrorNotSupported;
+    }
+    const std::int64_t strips = static_cast<std::int64_t>(batch) * channels * (height / patch);
+    const unsigned int grid = stride_grid(strips, 1, kStripBlocksPerCu);
+    auto run = [&](auto kernel) {
+        kernel<<<grid, kBlock, 0, stream>>>(images, patches, channels, height, width, strips);
+        return hipGetLastError();
+    };
+    switch (patch / 8) {
+    case 1: return run(extract_patches_strip_f32_to_bf16_kernel<1>);
+    case 2: return run(extract_patches_strip_f32_to_bf16_kernel<2>);
+    case 4: return run(extract_patches_strip_f32_to_bf16_kernel<4>);
+    case 8: return run(extract_patches_strip_f32_to_bf16_kernel<8>);
+    default: return hipErrorNotSupported;
+    }
+}
 
 hipError_t extract_patches(const void* images, void* patches, int element_size, int batch,
                            int channels, int height, int width, int patch, hipStream_t stream) {
