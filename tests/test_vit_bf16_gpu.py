@@ -237,3 +237,21 @@ def test_bf16_vit_base_batch_64_sequence(cuvit, oracle, device, tmp_path):
     for i in (0, 37, 63):
         alone = forward(single, images[i], 1, device)[0]
         require_exact(together[i], alone, f"bf16 ViT-Base image {i} of the batch differs from it alone")
+
+
+def test_bf16_one_pass_image_gather_equals_conversion_then_gather(cuvit, oracle, device, tmp_path):
+    """The bf16 model converts and gathers 16-byte aligned images in one pass;
+    images 4 bytes off that alignment take the conversion kernel and then the
+    bf16 gather. A value's rounding does not depend on where the gather moves
+    it, so the logits must be the same bits either way (ViT-Tiny/16, batch 2)."""
+    config, _, _, model = build(cuvit, oracle, tmp_path, 313, max_batch=2,
+                                config=tiny_config(cuvit), small=False)
+    images = np.concatenate([random_image(oracle, config, 60 + i) for i in range(2)])
+    one_pass = forward(model, images, 2, device)
+    flat = to_device(images, device).reshape(-1)
+    shifted = torch.empty(flat.numel() + 1, device=device)
+    shifted[1:] = flat
+    logits = torch.empty(2 * config.classes, device=device)
+    model.forward(shifted[1:], logits, 2)
+    two_pass = to_host(logits).reshape(2, config.classes)
+    require_exact(two_pass, one_pass, "the one-pass image gather changed the logits")
