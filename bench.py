@@ -16,9 +16,12 @@ each launch reads and writes cold HBM.
 
 Checked: before timing, one step's outputs are compared with the CPU oracle on
 the same inputs (gather, class token and positional add bit-exact; LayerNorm
-and softmax max-abs <= 1e-5); after timing, every set's gather and LayerNorm
-outputs again, each image's class-token row bit-exact, and every softmax row
-summing to one. A mismatch exits with status 3 and prints no JSON line.
+and softmax max-abs <= 1e-5). Then every set the timed steps write (step i
+writes set i % sets of each pool) is reset: gather and LayerNorm outputs to
+NaN, token sets to zero, softmax sets to their seeded logits. After timing,
+exactly those sets are checked: gather outputs bit-exact and LayerNorm within
+1e-5 of the oracle, each image's class-token row bit-exact, every softmax row
+a probability vector. A mismatch exits with status 3 and prints no JSON line.
 
 value        algorithmic bytes of one step / measured time of one step (GB/s);
              the K timed steps are one captured HIP graph, timed with HIP events
@@ -103,7 +106,10 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="bound on the CPU baseline's measured work")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    return p.parse_args()
+    args = p.parse_args()
+    if args.steps < 1 or args.warmup < 0:
+        p.error("--steps must be at least 1 and --warmup at least 0")
+    return args
 
 
 class Pools:
@@ -135,6 +141,21 @@ class Pools:
                        for _ in range(self.tok_sets)]
         self.pos = torch.from_numpy(inputs["pos"]).to(device)
         self.cls = torch.from_numpy(inputs["cls"]).to(device)
+        self.seeded_logits = self.logits[0].clone()
+
+    def reset_written(self, steps: int) -> None:
+        """Puts back, in every set that @p steps steps write, what a kernel
+        that did not run would leave detectable: NaN in the gather and
+        LayerNorm outputs, zeros in the token sets, the seeded logits in the
+        softmax sets."""
+        for i in written_sets(self.px_sets, steps):
+            self.patches[i].fill_(float("nan"))
+        for i in written_sets(self.ln_sets, steps):
+            self.ln_y[i].fill_(float("nan"))
+        for i in written_sets(self.tok_sets, steps):
+            self.tokens[i].zero_()
+        for i in written_sets(self.sm_sets, steps):
+            self.logits[i].copy_(self.seeded_logits)
 
     def launchers(self, cuvit):
         """name -> function(set_index) that enqueues one launch on the current stream."""
@@ -223,36 +244,67 @@ def check_first_step(torch, pools, expected) -> dict:
     return report
 
 
-def check_after_timing(torch, pools, expected) -> str:
-    """Every set after the timed steps, on the device: gather outputs bit-exact
-    and LayerNorm outputs within 1e-5 of the oracle (their inputs never
-    change), each image's class-token row equal to cls + pos[0] bit for bit
-    (the broadcast rewrites it every step before the add), every softmax row
-    in [0, 1] and summing to one within 1e-4 (the softmax runs in place, so
-    later steps apply it to probabilities)."""
+def written_sets(count: int, steps: int) -> range:
+    """The sets of a pool of @p count sets that @p steps steps write: step i
+    writes set i % count."""
+    return range(min(count, max(steps, 0)))
+
+
+def check_after_timing(torch, pools, expected, steps: int) -> str:
+    """The sets the @p steps timed steps wrote (reset before timing by
+    Pools.reset_written), on the device: gather outputs bit-exact and
+    LayerNorm outputs within 1e-5 of the oracle (their inputs never change),
+    each image's class-token row equal to cls + pos[0] bit for bit (the
+    broadcast rewrites it every step before the add), every softmax row in
+    [0, 1] and summing to one within 1e-4 (the softmax runs in place, so a set
+    written twice holds the softmax of probabilities; the seeded logits it was
+    reset to are not in [0, 1])."""
     device = pools.gamma.device
     patches = torch.from_numpy(expected["patches"].reshape(-1)).to(device)
     ln_y = torch.from_numpy(expected["ln_y"].reshape(-1)).to(device)
     row0 = torch.from_numpy(expected["tokens"].reshape(BATCH, TOKENS, EMBED)[:, 0, :].copy()).to(device)
-    for i in range(pools.px_sets):
+    checked = {"gather": written_sets(pools.px_sets, steps),
+               "LayerNorm": written_sets(pools.ln_sets, steps),
+               "token": written_sets(pools.tok_sets, steps),
+               "softmax": written_sets(pools.sm_sets, steps)}
+    if not all(len(sets) for sets in checked.values()):
+        raise CheckFailed(f"{steps} timed steps write no buffer set")
+    for i in checked["gather"]:
         if not torch.equal(pools.patches[i].view(torch.int32), patches.view(torch.int32)):
             raise CheckFailed(f"patch gather set {i} differs after timing")
-    for i in range(pools.ln_sets):
+    for i in checked["LayerNorm"]:
         worst = float((pools.ln_y[i] - ln_y).abs().max())
         if not worst <= MAX_ABS_FP32:
             raise CheckFailed(f"layer_norm set {i}: max-abs error {worst:.3g} after timing")
-    for i in range(pools.tok_sets):
+    for i in checked["token"]:
         got = pools.tokens[i].view(BATCH, TOKENS, EMBED)[:, 0, :]
         if not torch.equal(got.view(torch.int32), row0.view(torch.int32)):
             raise CheckFailed(f"class-token rows of token set {i} differ after timing")
-    for i in range(pools.sm_sets):
+    for i in checked["softmax"]:
         p = pools.logits[i].view(SOFTMAX_ROWS, TOKENS)
         sums = p.double().sum(dim=1)
         if not (bool(((p >= 0) & (p <= 1)).all()) and float((sums - 1).abs().max()) <= 1.0e-4):
             raise CheckFailed(f"softmax set {i}: a row is not a probability vector after timing")
     torch.cuda.synchronize()
-    return (f"{pools.px_sets} gather, {pools.ln_sets} LayerNorm, {pools.tok_sets} token and "
-            f"{pools.sm_sets} softmax sets checked after timing")
+    return ", ".join(f"{len(sets)} {name}" for name, sets in checked.items()) + \
+        " sets (every set the timed steps wrote) checked after timing"
+
+
+def checked_steps(torch, pools, launch, expected, steps: int, warmup: int, timer):
+    """The step sequence around the timed region: one step checked against
+    the oracle, @p warmup untimed steps, the written sets reset, @p steps
+    steps timed by @p timer (a function of the step body returning ms),
+    then the written sets checked. Returns (ms, checks); raises CheckFailed."""
+    pools.reset_written(1)
+    step(launch, 0)
+    checks = check_first_step(torch, pools, expected)
+    for i in range(warmup):
+        step(launch, i)
+    pools.reset_written(steps)
+    torch.cuda.synchronize()
+    ms = timer(lambda: [step(launch, i) for i in range(steps)])
+    checks["after_timing"] = check_after_timing(torch, pools, expected, steps)
+    return ms, checks
 
 
 def step(launch, i):
@@ -646,16 +698,10 @@ def main():
     launch = pools.launchers(cuvit)
     expected = expected_step(oracle, inputs)
     try:
-        step(launch, 0)
-        checks = check_first_step(torch, pools, expected)
-        for i in range(args.warmup):
-            step(launch, i)
-        torch.cuda.synchronize()
-
         # K timed steps, one graph, rotating sets.
-        ms_graph = timed_graph(torch, lambda: [step(launch, i) for i in range(args.steps)], 1)
+        ms_graph, checks = checked_steps(torch, pools, launch, expected, args.steps, args.warmup,
+                                         lambda body: timed_graph(torch, body, 1))
         ms_per_step = ms_graph / args.steps
-        checks["after_timing"] = check_after_timing(torch, pools, expected)
     except CheckFailed as failure:
         print(f"bench.py: output check failed: {failure}", file=sys.stderr, flush=True)
         sys.exit(3)
