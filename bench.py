@@ -438,8 +438,10 @@ def vit_forward(torch, cuvit, device, batch: int, replays: int, base: bool = Fal
 def vit_base_bf16(torch, cuvit, device):
     """ViT-Base/16 batch-64 shapes with bf16 activations: cold per-launch times
     of LN [12608, 768], softmax [151296, 197] in place, the patch gather
-    [64, 3, 224, 224], FC1 with the GELU epilogue (M 12608, N 3072, K 768) and
-    FC2 accumulating into the residual stream (M 12608, N 768, K 3072)."""
+    [64, 3, 224, 224], and the four linear layers: FC1 with the GELU epilogue
+    (M 12608, N 3072, K 768), FC2 accumulating into the residual stream (M
+    12608, N 768, K 3072), QKV (N 2304, K 768) and the projection accumulating
+    (N 768, K 768)."""
     rows, embed, hidden, heads, batch = 64 * TOKENS, 768, 3072, 12, 64
     bf = torch.bfloat16
     results = {}
@@ -497,6 +499,29 @@ def vit_base_bf16(torch, cuvit, device):
                 lambda i: cuvit.gemm(h[i], w, bias, residual[i], fc2), 2)
     results["fc2_gemm"]["TFLOPs"] = round(flops / (ms * 1e-3) / 1e12, 2)
     results["fc2_gemm"]["frac_of_bf16_mfma_peak"] = round(flops / (ms * 1e-3) / 2.5e15, 4)
+    del h
+    # QKV (M 12608, N 2304, K 768, bias) and the projection accumulating into
+    # the residual stream (M 12608, N 768, K 768).
+    x = [torch.randn(rows * embed, device=device).to(bf) for _ in range(2)]
+    w_qkv = (0.02 * torch.randn(3 * embed * embed, device=device)).to(bf)
+    b_qkv = 0.02 * torch.randn(3 * embed, device=device)
+    qkv = [torch.empty(rows * 3 * embed, device=device, dtype=bf) for _ in range(2)]
+    p_qkv = cuvit.gemm_problem(rows, 3 * embed, embed, cuvit.TRANSPOSED)
+    ms = record("qkv_gemm", 2 * (rows * embed + 3 * embed * embed + 3 * rows * embed),
+                lambda i: cuvit.gemm(x[i], w_qkv, b_qkv, qkv[i], p_qkv), 2)
+    qkv_flops = 2.0 * rows * 3 * embed * embed
+    results["qkv_gemm"]["TFLOPs"] = round(qkv_flops / (ms * 1e-3) / 1e12, 2)
+    results["qkv_gemm"]["frac_of_bf16_mfma_peak"] = round(qkv_flops / (ms * 1e-3) / 2.5e15, 4)
+    del qkv
+    w_proj = w_qkv[:embed * embed]
+    b_proj = b_qkv[:embed]
+    p_proj = cuvit.gemm_problem(rows, embed, embed, cuvit.TRANSPOSED)
+    p_proj.epilogue.accumulate = 1
+    ms = record("projection_gemm", 2 * (rows * embed + embed * embed + 2 * rows * embed),
+                lambda i: cuvit.gemm(x[i], w_proj, b_proj, residual[i], p_proj), 2)
+    proj_flops = 2.0 * rows * embed * embed
+    results["projection_gemm"]["TFLOPs"] = round(proj_flops / (ms * 1e-3) / 1e12, 2)
+    results["projection_gemm"]["frac_of_bf16_mfma_peak"] = round(proj_flops / (ms * 1e-3) / 2.5e15, 4)
     return results
 
 
@@ -553,7 +578,8 @@ def vit_base_bf16_counters(torch, cuvit, flush):
     """The ViT-Base batch-64 bf16 kernels for the counter passes, three cold
     launches each: LN [12608, 768], softmax [151296, 197] in place, the patch
     gather [64, 3, 224, 224], FC1 with the GELU epilogue, FC2 accumulating
-    into the residual stream (12608 x 768 x 3072) and the fused attention;
+    into the residual stream (12608 x 768 x 3072), QKV (12608 x 2304 x 768),
+    the projection accumulating (12608 x 768 x 768) and the fused attention;
     then the fp32 fused attention and the fp32 FC1 + GELU GEMM (6304 x 768 x
     192) at ViT-Tiny batch 32."""
     rows, embed, hidden, heads, batch = 64 * TOKENS, 768, 3072, 12, 64
@@ -575,6 +601,11 @@ def vit_base_bf16_counters(torch, cuvit, flush):
     fc2_problem = cuvit.gemm_problem(rows, embed, hidden, cuvit.TRANSPOSED)
     fc2_problem.epilogue.accumulate = 1
     qkv = torch.randn(rows * 3 * embed, device="cuda").to(bf)
+    # QKV reads W as [2304, 768] and the projection as [768, 768] (both inside
+    # W1's storage) and the bias's first 2304 / 768 values.
+    qkv_problem = cuvit.gemm_problem(rows, 3 * embed, embed, cuvit.TRANSPOSED)
+    proj_problem = cuvit.gemm_problem(rows, embed, embed, cuvit.TRANSPOSED)
+    proj_problem.epilogue.accumulate = 1
     context = torch.empty(rows * embed, device="cuda", dtype=bf)
     tiny_qkv = torch.randn(BATCH * TOKENS * 3 * 192, device="cuda")
     tiny_context = torch.empty(BATCH * TOKENS * 192, device="cuda")
@@ -592,6 +623,8 @@ def vit_base_bf16_counters(torch, cuvit, flush):
                                                                   IMAGE, IMAGE, PATCH),
         "bf16 fc1_gelu_gemm 12608x3072x768": lambda: cuvit.gemm(x, w, bias, c, problem),
         "bf16 fc2_gemm 12608x768x3072 accumulating": lambda: cuvit.gemm(c, w, bias, y, fc2_problem),
+        "bf16 qkv_gemm 12608x2304x768": lambda: cuvit.gemm(x, w, bias, qkv, qkv_problem),
+        "bf16 projection_gemm 12608x768x768 accumulating": lambda: cuvit.gemm(x, w, bias, y, proj_problem),
         "bf16 attention ViT-Base b64": lambda: cuvit.attention(qkv, context, batch, heads, TOKENS, 64),
         "fp32 attention ViT-Tiny b32": lambda: cuvit.attention(tiny_qkv, tiny_context, BATCH, 3,
                                                                TOKENS, 64),

@@ -14,6 +14,7 @@
 //        (32-deep stages up to K = 1024), else 64 x 64.
 // Every kernel of a type runs the same MFMA over K in the same order, so the
 // choice never changes a result.
+#include "gemm_dma.hpp"
 #include "gemm_kernel.hpp"
 #include "gemm_panel.hpp"
 #include "gemm_wide.hpp"
@@ -325,8 +326,120 @@ hipError_t launch_wide(const std::uint16_t* a, const std::uint16_t* b, const flo
     return args.alpha == 1.0F ? pick(std::false_type{}) : pick(std::true_type{});
 }
 
+/// The XCD split for a persistent kernel whose @p turns workgroups per XCD
+/// take an XCD's tiles in turn: fewest rounds (the largest block's tiles over
+/// @p turns), then the fewest bytes moved into the L2 caches (tile_map's
+/// measure). Measured at ViT-Base FC2 on 192 x 256 tiles: a byte-only choice
+/// left one XCD 34 tiles for its 32 workgroups, 139 against 88 us.
+gemm::TileMap balanced_map(const GemmArgs& args, int bm, int bn, int turns) {
+    const int tiles_m = (args.m + bm - 1) / bm;
+    const int tiles_n = (args.n + bn - 1) / bn;
+    const double a_bytes = static_cast<double>(tiles_m) * bm * args.k * 2;
+    const double b_bytes = static_cast<double>(tiles_n) * bn * args.k * 2;
+    constexpr double kL2Budget = 3.0 * (1 << 20);
+    gemm::TileMap best{0, 0};
+    double best_cost = 0.0;
+    int best_rounds = 0;
+    for (const int px : {8, 4, 2, 1}) {
+        const int py = 8 / px;
+        if (px > tiles_m || py > tiles_n) {
+            continue;
+        }
+        const int block = ((tiles_m + px - 1) / px) * ((tiles_n + py - 1) / py);
+        const int rounds = (block + turns - 1) / turns;
+        double cost = py * a_bytes + px * b_bytes;
+        if (b_bytes / py > kL2Budget) {
+            cost *= 2.0;
+        }
+        if (best.px == 0 || rounds < best_rounds || (rounds == best_rounds && cost < best_cost)) {
+            best = gemm::TileMap{px, py};
+            best_cost = cost;
+            best_rounds = rounds;
+        }
+    }
+    return best;
+}
+
+/// The direct-to-LDS kernel (gemm_dma.hpp) for a problem it covers: one batch
+/// entry, B as [N, K], N a multiple of 256, K of at least 256, no addend,
+/// vector A and B, C written in 16-byte pieces, every operand tile within one
+/// descriptor's span, the CUs a multiple of 8 (one persistent workgroup per
+/// CU, eight per XCD) and BM x 256 tiles for at least half the CUs. BM is the
+/// height with the fewest rounds x BM (ViT-Base b64: 320 for FC1, 256 for QKV,
+/// 192 for FC2 and the projection). Returns hipErrorNotSupported otherwise.
+hipError_t launch_dma(const std::uint16_t* a, const std::uint16_t* b, const float* bias,
+                      std::uint16_t* c, const GemmArgs& args, hipStream_t stream) {
+    const int units = compute_units();
+    const bool eligible =
+        args.transposed && args.count == 1 && args.addend == nullptr && args.rows_per_entry == 0 &&
+        args.n % 256 == 0 && args.k >= 256 && units % 8 == 0 &&
+        vector_operand(a, args.lda, args.k, 0, 0, false) && vector_operand(b, args.ldb, args.k, 0, 0, false) &&
+        static_cast<std::int64_t>(320) * args.lda * 2 < gemm::kMaxSpan &&
+        static_cast<std::int64_t>(256) * args.ldb * 2 < gemm::kMaxSpan && aligned16(c) &&
+        args.ldc % 8 == 0 && static_cast<std::int64_t>(args.n) * 4 < gemm::kMaxSpan;
+    if (!eligible) {
+        return hipErrorNotSupported;
+    }
+    int bm = 0;
+    std::int64_t best = 0;
+    for (const int height : {192, 256, 320}) {
+        const std::int64_t tiles = tile_count(args, height, 256);
+        const std::int64_t cost = (tiles + units - 1) / units * height;
+        if (bm == 0 || cost < best) {
+            bm = height;
+            best = cost;
+        }
+    }
+    if (2 * tile_count(args, bm, 256) < units) {
+        return hipErrorNotSupported;  // fewer tiles than half the CUs: the other kernels
+    }
+    const int turns = units / 8;
+    const gemm::TileMap map = balanced_map(args, bm, 256, turns);
+    auto run = [&](auto kernel, std::size_t lds_bytes) -> hipError_t {
+        static std::atomic<std::uint64_t> opted_in{0};
+        if (const hipError_t opted = allow_lds(reinterpret_cast<const void*>(kernel), lds_bytes, opted_in);
+            opted != hipSuccess) {
+            return opted;
+        }
+        kernel<<<units, 512, lds_bytes, stream>>>(a, b, bias, c, args, map);
+        return hipGetLastError();
+    };
+    // The epilogue's parts as template flags: bias, GELU, alpha (when not 1),
+    // accumulate.
+    auto pick = [&](auto height) -> hipError_t {
+        constexpr int BM = decltype(height)::value;
+        constexpr std::size_t kLds = gemm::DmaShape<BM>::kLdsBytes;
+        auto with_flags = [&](auto with_bias, auto with_gelu, auto with_alpha) -> hipError_t {
+            constexpr bool kB = decltype(with_bias)::value;
+            constexpr bool kG = decltype(with_gelu)::value;
+            constexpr bool kA = decltype(with_alpha)::value;
+            return args.accumulate ? run(gemm::gemm_dma_kernel<BM, kB, kG, kA, true>, kLds)
+                                   : run(gemm::gemm_dma_kernel<BM, kB, kG, kA, false>, kLds);
+        };
+        auto with_alpha = [&](auto with_bias, auto with_gelu) -> hipError_t {
+            return args.alpha == 1.0F ? with_flags(with_bias, with_gelu, std::false_type{})
+                                      : with_flags(with_bias, with_gelu, std::true_type{});
+        };
+        auto with_gelu = [&](auto with_bias) -> hipError_t {
+            return args.gelu ? with_alpha(with_bias, std::true_type{}) : with_alpha(with_bias, std::false_type{});
+        };
+        return bias != nullptr ? with_gelu(std::true_type{}) : with_gelu(std::false_type{});
+    };
+    switch (bm) {
+    case 192: return pick(std::integral_constant<int, 192>{});
+    case 256: return pick(std::integral_constant<int, 256>{});
+    default: return pick(std::integral_constant<int, 320>{});
+    }
+}
+
 hipError_t gemm_bf16(const std::uint16_t* a, const std::uint16_t* b, const float* bias,
                      std::uint16_t* c, const GemmArgs& args, hipStream_t stream) {
+    // The direct-to-LDS kernel where it applies (ViT-Base b64 against the
+    // kernels below, same bits: FC1 + GELU 101 -> 92 us, QKV 68 -> 51, FC2
+    // accumulating 85 -> 77, the projection 39 -> 26).
+    if (const hipError_t dma = launch_dma(a, b, bias, c, args, stream); dma != hipErrorNotSupported) {
+        return dma;
+    }
     // 128 x 256 tiles with 64 x 128 per wavefront (ViT-Base FC1 + GELU 137 ->
     // 110 us), where they apply; bitwise the same results as the tiles below.
     if (const hipError_t wide = launch_wide<2, 4>(a, b, bias, c, args, stream);
