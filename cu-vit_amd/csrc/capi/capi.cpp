@@ -504,6 +504,21 @@ int cuvit_extract_patches_bf16(const cuvit_bf16* images, cuvit_bf16* patches, in
                     "extract_patches launch");
 }
 
+int cuvit_extract_patches_f32_to_bf16(const float* images, cuvit_bf16* patches, int batch,
+                                      int channels, int height, int width, int patch,
+                                      cuvit_stream_t stream) {
+    bool empty = false;
+    if (const int s = capi::check_patches(images, patches, batch, channels, height, width, patch,
+                                          &empty);
+        s != CUVIT_OK || empty) {
+        return s;
+    }
+    return from_hip(detail::extract_patches_f32_to_bf16_any(images, patches, batch, channels,
+                                                            height, width, patch,
+                                                            capi::as_hip(stream)),
+                    "extract_patches launch");
+}
+
 void cuvit_preprocessing_default(cuvit_preprocessing* settings) {
     if (settings == nullptr) {
         return;

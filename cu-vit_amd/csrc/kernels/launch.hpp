@@ -53,6 +53,11 @@ hipError_t extract_patches(const void* images, void* patches, int element_size, 
 hipError_t extract_patches_f32_to_bf16(const float* images, std::uint16_t* patches, int batch,
                                       int channels, int height, int width, int patch,
                                       hipStream_t stream);
+/// The same for any alignment and geometry: the strip kernel where it
+/// applies, else one element per thread.
+hipError_t extract_patches_f32_to_bf16_any(const float* images, std::uint16_t* patches, int batch,
+                                          int channels, int height, int width, int patch,
+                                          hipStream_t stream);
 hipError_t broadcast_f32(float* destination, const float* source, std::int64_t count,
                          std::int64_t destination_stride, int batch, hipStream_t stream);
 hipError_t broadcast_bf16(std::uint16_t* destination, const std::uint16_t* source,

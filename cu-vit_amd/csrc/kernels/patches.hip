@@ -285,10 +285,18 @@ __global__ __launch_bounds__(kWave) void extract_patches_pair_kernel(
     }
 }
 
-/// One element per iteration, any geometry and alignment.
-template <typename Word>
+/// Stores one gathered value: as it is, or an fp32 value rounded to bf16 bits.
+__device__ __forceinline__ void store_value(std::uint32_t* out, std::uint32_t word) { *out = word; }
+__device__ __forceinline__ void store_value(std::uint16_t* out, std::uint16_t word) { *out = word; }
+__device__ __forceinline__ void store_value(std::uint16_t* out, float value) {
+    *out = float_to_bf16(value);
+}
+
+/// One element per iteration, any geometry and alignment. @p In and @p Out
+/// are the same word (a bit-exact move) or fp32 in and bf16 bits out.
+template <typename In, typename Out>
 __global__ __launch_bounds__(kBlock) void extract_patches_element_kernel(
-    const Word* __restrict__ images, Word* __restrict__ patches, int channels, int height,
+    const In* __restrict__ images, Out* __restrict__ patches, int channels, int height,
     int width, int patch, std::int64_t total) {
     const std::int64_t patch_area = static_cast<std::int64_t>(patch) * patch;
     const std::int64_t row_length = channels * patch_area;
@@ -313,7 +321,7 @@ __global__ __launch_bounds__(kBlock) void extract_patches_element_kernel(
             ((image * channels + channel) * height + patch_row * patch + local_row) *
                 static_cast<std::int64_t>(width) +
             patch_column * patch + local_column;
-        patches[index] = images[source];
+        store_value(patches + index, images[source]);
     }
 }
 
@@ -432,7 +440,7 @@ hipError_t dispatch_patches(const void* images, void* patches, int batch, int ch
     using Word = std::conditional_t<ElementSize == 4, std::uint32_t, std::uint16_t>;
     const std::int64_t total = static_cast<std::int64_t>(batch) * channels * height * width;
     const unsigned int grid = stride_grid(total, kBlock, 16);
-    extract_patches_element_kernel<Word><<<grid, kBlock, 0, stream>>>(
+    extract_patches_element_kernel<Word, Word><<<grid, kBlock, 0, stream>>>(
         static_cast<const Word*>(images), static_cast<Word*>(patches), channels, height, width,
         patch, total);
     return hipGetLastError();
@@ -459,6 +467,21 @@ hipError_t extract_patches_f32_to_bf16(const float* images, std::uint16_t* patch
     case 8: return run(extract_patches_strip_f32_to_bf16_kernel<8>);
     default: return hipErrorNotSupported;
     }
+}
+
+hipError_t extract_patches_f32_to_bf16_any(const float* images, std::uint16_t* patches, int batch,
+                                          int channels, int height, int width, int patch,
+                                          hipStream_t stream) {
+    const hipError_t strips = extract_patches_f32_to_bf16(images, patches, batch, channels, height,
+                                                          width, patch, stream);
+    if (strips != hipErrorNotSupported) {
+        return strips;
+    }
+    const std::int64_t total = static_cast<std::int64_t>(batch) * channels * height * width;
+    const unsigned int grid = stride_grid(total, kBlock, 16);
+    extract_patches_element_kernel<float, std::uint16_t><<<grid, kBlock, 0, stream>>>(
+        images, patches, channels, height, width, patch, total);
+    return hipGetLastError();
 }
 
 hipError_t extract_patches(const void* images, void* patches, int element_size, int batch,

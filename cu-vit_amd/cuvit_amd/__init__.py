@@ -21,7 +21,8 @@ from typing import Optional
 __all__ = [
     "CuvitError", "InvalidArgument", "LengthError", "HipError", "OutOfRange",
     "GemmProblem", "VitConfig", "library", "library_path", "check", "stream_handle",
-    "gemm", "layer_norm", "softmax", "gelu", "extract_patches", "add", "add_broadcast",
+    "gemm", "layer_norm", "softmax", "gelu", "extract_patches", "extract_patches_f32_to_bf16",
+    "add", "add_broadcast",
     "broadcast", "convert_to_bf16", "convert_to_f32", "attention", "attention_supported",
     "gemm_problem", "WeightWriter", "WeightFile", "VisionTransformer",
     "NO_TRANSPOSE", "TRANSPOSED", "PRECISION_F32", "PRECISION_BF16",
@@ -175,6 +176,7 @@ _SIGNATURES = {
     "cuvit_softmax_bf16": (_I, [_P, _P, _I, _I, _P]),
     "cuvit_extract_patches_f32": (_I, [_P, _P, _I, _I, _I, _I, _I, _P]),
     "cuvit_extract_patches_bf16": (_I, [_P, _P, _I, _I, _I, _I, _I, _P]),
+    "cuvit_extract_patches_f32_to_bf16": (_I, [_P, _P, _I, _I, _I, _I, _I, _P]),
     "cuvit_add_f32": (_I, [_P, _P, _L, _P]),
     "cuvit_add_broadcast_f32": (_I, [_P, _P, _L, _I, _P]),
     "cuvit_broadcast_f32": (_I, [_P, _P, _L, _L, _I, _P]),
@@ -420,6 +422,18 @@ def extract_patches(images, patches, batch: int, channels: int, height: int, wid
         patches = _operand(patches, "patches", _storage(bf16), n)
     check(fn(_ptr(images), _ptr(patches), batch, channels, height, width, patch,
              stream_handle(stream)))
+
+
+def extract_patches_f32_to_bf16(images, patches, batch: int, channels: int, height: int,
+                                width: int, patch: int, stream=None) -> None:
+    """fp32 images into bf16 patch rows in one pass (bitwise the conversion
+    then the bf16 gather)."""
+    if _positive(batch, channels, height, width, patch):
+        n = batch * channels * height * width
+        images = _operand(images, "images", "float32", n)
+        patches = _operand(patches, "patches", _storage(True), n)
+    check(library().cuvit_extract_patches_f32_to_bf16(_ptr(images), _ptr(patches), batch, channels,
+                                                      height, width, patch, stream_handle(stream)))
 
 
 def add(accumulator, addend, count: int, stream=None) -> None:

@@ -177,6 +177,14 @@ int cuvit_convert_f32_to_bf16(const float* input, cuvit_bf16* output, int64_t co
                               cuvit_stream_t stream);
 int cuvit_convert_bf16_to_f32(const cuvit_bf16* input, float* output, int64_t count,
                               cuvit_stream_t stream);
+/* fp32 images gathered into bf16 patch rows in one pass, no counterpart in the
+ * reference: bitwise cuvit_convert_f32_to_bf16 of the images followed by
+ * cuvit_extract_patches_bf16, without the bf16 image copy in between (the
+ * bf16 model's image intake). Any alignment and geometry; validation is
+ * extract_patches'. */
+int cuvit_extract_patches_f32_to_bf16(const float* images, cuvit_bf16* patches, int batch,
+                                      int channels, int height, int width, int patch,
+                                      cuvit_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Weight files: the reference's .cvw v1 format (weights.hpp:16-92,

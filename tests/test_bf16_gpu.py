@@ -80,6 +80,45 @@ def test_extract_patches_bf16_bit_exact(cuvit, oracle, device, batch, size, patc
     require_exact(bf16_bits(y).reshape(expected.shape), expected, "bf16 patch gather")
 
 
+@pytest.mark.parametrize("batch,channels,size,patch,offset", [
+    (64, 3, 224, 16, 0),  # ViT-Base/16 batch 64: two 16-byte vectors per patch row
+    (3, 3, 64, 32, 0),    # four vectors per patch row
+    (2, 1, 128, 64, 0),   # eight vectors per patch row, one channel
+    (2, 4, 96, 32, 0),    # four channels, 3 x 3 patches
+    (3, 2, 40, 8, 0),     # one vector per patch row
+    (2, 3, 64, 32, 1),    # images one float off 16-byte alignment (element kernel)
+    (2, 3, 36, 12, 0),    # a patch width that is not a multiple of 8 (element kernel)
+])
+def test_extract_patches_f32_to_bf16_one_pass(cuvit, oracle, device, batch, channels, size, patch,
+                                              offset):
+    """fp32 images into bf16 patch rows in one pass: bitwise the conversion
+    followed by the bf16 gather, and bitwise the oracle's gather of the
+    images rounded to nearest-even (ties, signed zeros and infinities
+    planted)."""
+    count = batch * channels * size * size
+    images = oracle.generator(515 + size + patch).normal(count, 0.0, 2.0)
+    images[::97] = np.float32(1.0 + 2.0 ** -8)    # halfway between two bf16 values: even
+    images[5::97] = np.float32(1.0 + 3 * 2.0 ** -8)  # halfway: rounds up to even
+    images[7::211] = -0.0
+    images[11::509] = np.inf
+    images[13::509] = -np.inf
+    flat = to_device(images, device)
+    if offset:
+        shifted = torch.empty(count + offset, device=device)
+        shifted[offset:] = flat
+        flat = shifted[offset:]
+    one_pass = torch.empty(count, dtype=torch.bfloat16, device=device)
+    cuvit.extract_patches_f32_to_bf16(flat, one_pass, batch, channels, size, size, patch)
+    converted = torch.empty(count, dtype=torch.bfloat16, device=device)
+    cuvit.convert_to_bf16(flat, converted, count)
+    two_pass = torch.empty_like(converted)
+    cuvit.extract_patches(converted, two_pass, batch, channels, size, size, patch)
+    got = bf16_bits(one_pass)
+    require_exact(got, bf16_bits(two_pass), "one-pass gather vs conversion then bf16 gather")
+    expected = oracle.round_bf16(oracle.extract_patches(images, batch, channels, size, size, patch))
+    require_exact(got, expected.reshape(-1), "one-pass gather vs the oracle's rounded gather")
+
+
 def require_gemm_close(actual, expected, scale, context):
     """|a - e| <= 1e-2 |e| + 1e-5 * sum|terms| (bf16 output rounding plus the
     accumulation-order difference)."""
