@@ -18,9 +18,11 @@
 #include "cuvit/vit.hpp"
 
 #include "cuvit/capi.h"
+#include "cuvit/device_arena.hpp"
 #include "cuvit/hip_check.hpp"
 #include "cuvit/host_buffer.hpp"
 #include "cuvit/kernels.hpp"
+#include "cuvit/stream.hpp"
 
 #include "../capi/status.hpp"
 
@@ -442,14 +444,18 @@ void VisionTransformer::run_block(const BlockWeights& block,
     launch_gemm(stored.hidden, matrices.fc2, block.fc2_bias, tokens, fc2, stream);
 }
 
-void VisionTransformer::forward(const float* images, float* logits, int batch, hipStream_t stream) {
-    if (batch == 0) {
-        return;
-    }
+void VisionTransformer::check_batch(long long batch) const {
     if (batch < 0 || batch > max_batch_) {
         throw std::invalid_argument("This model was built for at most " + std::to_string(max_batch_) +
                                     " images, but " + std::to_string(batch) + " were given");
     }
+}
+
+void VisionTransformer::forward(const float* images, float* logits, int batch, hipStream_t stream) {
+    if (batch == 0) {
+        return;
+    }
+    check_batch(batch);
     if (images == nullptr || logits == nullptr) {
         throw std::invalid_argument("Forward pass operands cannot be null");
     }
@@ -527,25 +533,34 @@ void VisionTransformer::forward_stored(Stored<T>& stored, const float* images, f
 }
 
 std::vector<float> VisionTransformer::forward(const std::vector<float>& images) {
+    // Contract (vit.hpp:78-80 of the reference): host images in, host logits
+    // out, synchronized; the batch is the number of whole images given.
     const std::size_t per_image = image_elements();
     if (per_image == 0 || images.size() % per_image != 0) {
         throw std::invalid_argument("The input holds " + std::to_string(images.size()) +
                                     " elements, which is not a whole number of " +
                                     std::to_string(per_image) + "-element images");
     }
-    const std::size_t batch = images.size() / per_image;
-    if (batch > static_cast<std::size_t>(max_batch_)) {
-        throw std::invalid_argument("This model was built for at most " + std::to_string(max_batch_) +
-                                    " images, but " + std::to_string(batch) + " were given");
+    const auto batch = static_cast<long long>(images.size() / per_image);
+    check_batch(batch);
+    const std::size_t logit_count = static_cast<std::size_t>(batch) * config_.classes;
+    std::vector<float> logits(logit_count);
+    if (batch == 0) {
+        return logits;
     }
 
-    DeviceBuffer<float> device_images(images.size());
-    DeviceBuffer<float> device_logits(batch * static_cast<std::size_t>(config_.classes));
+    // Images and logits share one device block, each on its own 256-byte
+    // granule; it is released when the call returns, after the stream drains.
+    DeviceArena io(DeviceArena::reserved_bytes<float>(images.size()) +
+                   DeviceArena::reserved_bytes<float>(logit_count));
+    float* device_images = io.allocate_raw<float>(images.size());
+    float* device_logits = io.allocate_raw<float>(logit_count);
     Stream stream;
-    device_images.copy_from_host_async(images.data(), images.size(), stream.get());
-    forward(device_images.data(), device_logits.data(), static_cast<int>(batch), stream.get());
-    std::vector<float> logits(batch * static_cast<std::size_t>(config_.classes));
-    device_logits.copy_to_host_async(logits.data(), logits.size(), stream.get());
+    CUVIT_HIP_CHECK(hipMemcpyAsync(device_images, images.data(), images.size() * sizeof(float),
+                                   hipMemcpyHostToDevice, stream.get()));
+    forward(device_images, device_logits, static_cast<int>(batch), stream.get());
+    CUVIT_HIP_CHECK(hipMemcpyAsync(logits.data(), device_logits, logit_count * sizeof(float),
+                                   hipMemcpyDeviceToHost, stream.get()));
     stream.synchronize();
     return logits;
 }

@@ -117,6 +117,8 @@ class VisionTransformer final {
         T* logits = nullptr; // the head's output before widening (bf16 only)
     };
 
+    /// Throws std::invalid_argument unless 0 <= @p batch <= max_batch().
+    void check_batch(long long batch) const;
     template <typename T> void load(const WeightFile& file, Stored<T>& stored);
     template <typename T> void reserve_activations(Stored<T>& stored);
     template <typename T>
