@@ -80,6 +80,26 @@ def test_extract_patches_bf16_bit_exact(cuvit, oracle, device, batch, size, patc
     require_exact(bf16_bits(y).reshape(expected.shape), expected, "bf16 patch gather")
 
 
+@pytest.mark.parametrize("batch,channels,height", [
+    (1, 3, 224),    # 42 strips: the last group of four holds two
+    (5, 1, 96),     # one channel, 6 strips per image, not square
+    (7, 2, 32),     # two strips per plane
+    (200, 3, 224),  # 8400 strips: persistent workgroups take several turns
+])
+def test_extract_patches_bf16_staged_strips(cuvit, oracle, device, batch, channels, height):
+    """bf16 images 224 wide in 16 x 16 patches take the LDS-staged strip
+    kernel (four strips a turn, persistent workgroups); every strip count and
+    turn count must land bit for bit where the oracle's permutation puts it."""
+    width = 224
+    bits, _ = bf16_inputs(oracle, 507 + batch, batch * channels * height * width)
+    expected = oracle.extract_patches(bits.astype(np.float32), batch, channels, height, width,
+                                      16).astype(np.uint16)
+    x = bf16_tensor(bits, device)
+    y = torch.full_like(x, float("nan"))
+    cuvit.extract_patches(x, y, batch, channels, height, width, 16)
+    require_exact(bf16_bits(y).reshape(expected.shape), expected, "staged bf16 patch gather")
+
+
 @pytest.mark.parametrize("batch,channels,size,patch,offset", [
     (64, 3, 224, 16, 0),  # ViT-Base/16 batch 64: two 16-byte vectors per patch row
     (3, 3, 64, 32, 0),    # four vectors per patch row
