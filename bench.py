@@ -36,6 +36,7 @@ copy ceiling the library's bench-only copy kernel (libcuvit_bench.so: eight
 vit_tiny_forward  the full batch-32 forward (89 launches: attention fused, positional add in the embedding GEMM) as one HIP graph.
 vit_*_forward_bf16 the bf16 model: ViT-Tiny at batch 32 and ViT-Base at batch 64.
 vit_base_b64_bf16 the bf16 twins at ViT-Base/16 batch-64 shapes, cold.
+attention    the fused attention, cold: bf16 at ViT-Base b64, fp32 at ViT-Tiny b32.
 size_sweep   LN, softmax and the gather at ViT-Tiny shapes for batches 32-1024,
              each beside a same-bytes copy.
 cpu_baseline the CPU oracle (a restatement of the reference's CPU loops) on
@@ -525,6 +526,32 @@ def vit_base_bf16(torch, cuvit, device):
     return results
 
 
+def attention_block(torch, cuvit, device):
+    """The fused attention per launch, cold (rotating pools of the packed QKV
+    projection): bf16 at ViT-Base/16 batch 64 (768 (image, head) pairs) and
+    fp32 at ViT-Tiny/16 batch 32 (96 pairs). Bytes: the QKV rows read once and
+    the context written once; flops: 4 T^2 64 per pair (logits and weights.V)."""
+    results = {}
+    for name, dtype, batch, heads, peak in (("bf16_vit_base_b64", torch.bfloat16, 64, 12, 2.5e15),
+                                            ("fp32_vit_tiny_b32", torch.float32, BATCH, 3, 157.3e12)):
+        embed = heads * 64
+        count = batch * TOKENS * 3 * embed
+        size = 2 if dtype == torch.bfloat16 else 4
+        sets = max(2, -(-POOL_BYTES // (count * size)))
+        qkv = [torch.randn(count, device=device).to(dtype) for _ in range(sets)]
+        context = [torch.empty(batch * TOKENS * embed, device=device, dtype=dtype) for _ in range(2)]
+        ms = timed_graph(torch, lambda: [cuvit.attention(qkv[i], context[i % 2], batch, heads, TOKENS, 64)
+                                         for i in range(sets)], max(1, 200 // sets)) / sets
+        nbytes = batch * TOKENS * 4 * embed * size
+        flops = 4.0 * TOKENS * TOKENS * 64 * batch * heads
+        results[name] = {"us_per_launch": round(ms * 1e3, 3), "bytes": nbytes,
+                         "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                         "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 2),
+                         "frac_of_mfma_peak": round(flops / (ms * 1e-3) / peak, 4)}
+        del qkv, context
+    return results
+
+
 def cpu_baseline(seconds: float, oracle, inputs):
     """The CPU oracle over the same workload on the same seeded inputs, one
     core, whole steps until @p seconds of measured work (at least one step)."""
@@ -821,6 +848,7 @@ def main():
                     "fused (bitwise equal to the bf16 GEMM -> softmax -> GEMM launches); MFMA bf16 "
                     "dense peak 2.5 PFLOP/s"}
     line["vit_base_b64_bf16"] = vit_base_bf16(torch, cuvit, device)
+    line["attention"] = attention_block(torch, cuvit, device)
     line["size_sweep"] = size_sweep(torch, cuvit, device)
     line["preprocess"] = preprocess_block(torch, cuvit, device)
     if not args.no_cpu:

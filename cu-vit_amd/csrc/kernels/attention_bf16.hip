@@ -172,10 +172,19 @@ __device__ __forceinline__ PairBases pair_bases(const std::uint16_t* qkv, int pa
 /// @tparam Chunks per thread of a pair's K and V (ceil(2 * KT * 32 * 8 / threads)) when the
 ///   workgroup loops over several pairs and prefetches the next pair's K and V into
 ///   registers while it works on the current one; 0 for one pair per workgroup.
-template <int KT, int Chunks>
+/// @tparam kTokens the token count when it is fixed at compile time (197,
+///   the ViT/16 count at 224), 0 otherwise: the runs of the last key tile
+///   that lie wholly past it are then known to be zero, and their logits
+///   skip the max, the exponential, the sum and the probability (a sum of
+///   non-negative terms from +0 is unchanged by adding +0).
+template <int KT, int Chunks, int kTokens = 0>
 __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
     const std::uint16_t* __restrict__ qkv, std::uint16_t* __restrict__ context, int heads,
-    int tokens, int pairs) {
+    int tokens_argument, int pairs) {
+    const int tokens = kTokens > 0 ? kTokens : tokens_argument;
+    // Run q of key tile kt holds keys kt * 32 + 8 q + 4 half + 0..3: with
+    // the token count known, a run whose first key is past it is all past it.
+    auto run_past = [](int kt, int q) { return kTokens > 0 && kt * kEdge + 8 * q >= kTokens; };
     constexpr int kPadded = KT * kEdge;
     constexpr int kBufferElements = kPadded * (kHeadDim + kKeyPitch);
     extern __shared__ Vec16 lds_vectors[];
@@ -340,12 +349,15 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
         for (int i = 0; i < 16; ++i) {
             const int key = kt * kEdge + Bf16Mma::column(lane, i / 4) + i % 4;
             // Only the last key tile holds keys past the tokens.
-            if (kt < KT - 1 || key < tokens) {
+            if (!run_past(kt, i / 4) && (kt < KT - 1 || key < tokens)) {
                 maximum = fmaxf(maximum, x[kt][i]);
             }
         }
 #pragma unroll
         for (int i = 0; i < 16; i += 2) {
+            if (run_past(kt, i / 4)) {
+                continue;
+            }
             const std::uint32_t bits = pack_bf16x2(x[kt][i], x[kt][i + 1]);
             x[kt][i] = __uint_as_float(bits << 16);
             x[kt][i + 1] = __uint_as_float(bits & 0xFFFF0000U);
@@ -354,14 +366,17 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
     maximum = bf16_to_float(float_to_bf16(maximum));
     maximum = combine_halves(maximum, [](float a, float b) { return fmaxf(a, b); });
 
-    // Exponentials; keys past the tokens are 0, as the softmax sets them.
+    // Exponentials in the bf16 softmax's fused form (softmax_terms.hpp),
+    // exp2(x * c + shift) with shift = -(max * c) rounded once, where c
+    // carries the 1/8; keys past the tokens are 0, as the softmax sets them.
+    const float shift = -(maximum * kScaledLog2e);
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int key = kt * kEdge + Bf16Mma::column(lane, i / 4) + i % 4;
-            x[kt][i] = kt < KT - 1 || key < tokens
-                           ? __builtin_amdgcn_exp2f((x[kt][i] - maximum) * kScaledLog2e)
+            x[kt][i] = !run_past(kt, i / 4) && (kt < KT - 1 || key < tokens)
+                           ? __builtin_amdgcn_exp2f(fmaf(x[kt][i], kScaledLog2e, shift))
                            : 0.F;
         }
     }
@@ -377,7 +392,9 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
             float sum = 0.F;
 #pragma unroll
             for (int j = 0; j < 2 * KT; ++j) {
-                sum += x[j / 2][4 * (g + 2 * (j % 2)) + r];
+                if (!run_past(j / 2, g + 2 * (j % 2))) {
+                    sum += x[j / 2][4 * (g + 2 * (j % 2)) + r];
+                }
             }
             part[r] = sum;
         }
@@ -397,6 +414,11 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void attention_bf16_kernel(
     for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
         for (int run = 0; run < 4; ++run) {
+            if (run_past(kt, run)) {
+                p[kt][run][0] = 0U;  // 0 * inverse, rounded: +0
+                p[kt][run][1] = 0U;
+                continue;
+            }
             p[kt][run][0] = pack_bf16(x[kt][4 * run] * inverse, x[kt][4 * run + 1] * inverse);
             p[kt][run][1] = pack_bf16(x[kt][4 * run + 2] * inverse, x[kt][4 * run + 3] * inverse);
         }
@@ -501,17 +523,27 @@ hipError_t launch(const std::uint16_t* qkv, std::uint16_t* context, int images, 
         // buffer after it: each CU's later pairs do not wait for their loads.
         // With waves = KT, a thread's share of a pair's K and V is 8 chunks.
         constexpr int kChunksPerThread = 2 * kEdge * kChunksPerKey / kWave;
-        auto kernel = attention_bf16_kernel<KT, kChunksPerThread>;
-        static std::atomic<std::uint64_t> opted_in{0};
-        if (const hipError_t opted =
-                allow_lds(reinterpret_cast<const void*>(kernel), 2 * lds_bytes(KT), opted_in);
-            opted != hipSuccess) {
-            return opted;
-        }
         const std::int64_t groups = compute_units() < pairs ? compute_units() : pairs;
-        kernel<<<dim3(1, static_cast<unsigned int>(groups)), query_tiles * kWave, 2 * lds_bytes(KT),
-                 stream>>>(qkv, context, heads, tokens, static_cast<int>(pairs));
-        return hipGetLastError();
+        auto run = [&](auto kernel, std::atomic<std::uint64_t>& opted_in) -> hipError_t {
+            if (const hipError_t opted =
+                    allow_lds(reinterpret_cast<const void*>(kernel), 2 * lds_bytes(KT), opted_in);
+                opted != hipSuccess) {
+                return opted;
+            }
+            kernel<<<dim3(1, static_cast<unsigned int>(groups)), query_tiles * kWave,
+                     2 * lds_bytes(KT), stream>>>(qkv, context, heads, tokens, static_cast<int>(pairs));
+            return hipGetLastError();
+        };
+        // 197 tokens (ViT/16 at 224) with the count as a constant: the last
+        // key tile's runs past it cost nothing.
+        if constexpr (KT == 7) {
+            if (tokens == 197) {
+                static std::atomic<std::uint64_t> opted_in{0};
+                return run(attention_bf16_kernel<KT, kChunksPerThread, 197>, opted_in);
+            }
+        }
+        static std::atomic<std::uint64_t> opted_in{0};
+        return run(attention_bf16_kernel<KT, kChunksPerThread>, opted_in);
     }
     }
     // Above 64 KiB (256 tokens) the kernel opts in to more LDS, once per device.

@@ -40,7 +40,12 @@
 // exponential grows only with |x - max| (about |x - max| * 2^-23 plus the exp2
 // unit's ~1 ulp), so it is largest where the output is smallest: under 1e-6
 // absolute for every output, far inside the reference test's 1e-4 relative
-// tolerance (tests/elementwise_test.cu:254-255).
+// tolerance (tests/elementwise_test.cu:254-255). bf16 rows of the register and
+// staged paths take exp2(fma(x, log2 e, -(max * log2 e))) instead, one
+// instruction a term fewer (the fused bf16 attention does the same, so the two
+// stay bitwise equal): the shift's rounding moves an exponent by at most an
+// ulp of max * log2 e, a relative change of about 1e-7 in the output against
+// bf16's 4e-3 spacing.
 //
 // Streaming path (rows wider than the register path holds): one wavefront per
 // row with an online max: a single streaming pass keeps a running (max, sum)
@@ -88,7 +93,7 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_kernel(const T* input, T*
             const int column = t + L * j;
             x[j] = here && column < columns ? Elem<T>::load_streaming(source + column) : -INFINITY;
         }
-        softmax_terms<L, J>(x, t, columns);
+        softmax_terms<L, J, sizeof(T) == 2>(x, t, columns);
         if (here) {
 #pragma unroll
             for (int j = 0; j < J; ++j) {
@@ -197,7 +202,7 @@ __global__ __launch_bounds__(kBlock) void softmax_staged_kernel(const T* input, 
                 x[j] = here && column < columns ? Elem<T>::load(tile_elements + r * columns + column)
                                                 : -INFINITY;
             }
-            softmax_terms<L, J>(x, t, columns);
+            softmax_terms<L, J, sizeof(T) == 2>(x, t, columns);
             if (here) {
 #pragma unroll
                 for (int j = 0; j < J; ++j) {

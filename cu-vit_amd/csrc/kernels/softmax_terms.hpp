@@ -4,7 +4,10 @@
 // A row is reduced by a team of L lanes (16: one DPP row; 64: the wavefront):
 // column c is lane c % L's (c / L)-th term, the lane folds its terms in order
 // from +0, then a fixed DPP tree combines the team. Exponentials are
-// exp2((x - max) * log2 e) on the hardware exp2.
+// exp2((x - max) * log2 e) on the hardware exp2 for fp32 rows, and
+// exp2(fma(x, log2 e, -(max * log2 e))) for bf16 rows (one instruction a term
+// fewer: the row's shift is formed once; its rounding moves the exponent by at
+// most an ulp of max * log2 e, far below the bf16 rounding of the result).
 #pragma once
 
 #include "device_common.hpp"
@@ -28,11 +31,18 @@ template <int L, typename Op> __device__ __forceinline__ float team_allreduce(fl
     }
 }
 
+/// exp(x - max) as exp2(x * log2 e + shift), shift = -(max * log2 e) rounded
+/// once, the product kept exact by the fused multiply-add (the bf16 rows' form).
+__device__ __forceinline__ float shifted_exp_fused(float x, float shift) {
+    return __builtin_amdgcn_exp2f(fmaf(x, kLog2e, shift));
+}
+
 /// Softmax of one row whose J terms per lane are in @p x (-inf past the row):
 /// on return x holds the outputs. Team lane @p t holds columns t + L * j.
 /// J may exceed the row's need: a term past the row is -inf before and 0
 /// after the exponential, which changes no bit of the max or the sum.
-template <int L, int J>
+/// @tparam kFused the bf16 rows' exponential (shifted_exp_fused).
+template <int L, int J, bool kFused = false>
 __device__ __forceinline__ void softmax_terms(float (&x)[J], int t, int columns) {
     float maximum = x[0];
 #pragma unroll
@@ -40,10 +50,12 @@ __device__ __forceinline__ void softmax_terms(float (&x)[J], int t, int columns)
         maximum = fmaxf(maximum, x[j]);
     }
     const float row_maximum = team_allreduce<L>(maximum, Max{});
+    const float shift = -(row_maximum * kLog2e);
     float sum = 0.F;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        x[j] = t + L * j < columns ? shifted_exp(x[j], row_maximum) : 0.F;
+        const float e = kFused ? shifted_exp_fused(x[j], shift) : shifted_exp(x[j], row_maximum);
+        x[j] = t + L * j < columns ? e : 0.F;
         sum += x[j];
     }
     const float inverse = 1.0F / team_allreduce<L>(sum, Sum{});

@@ -152,7 +152,9 @@ def bf16_qkv(oracle, seed, count, device, stddev=1.0):
 
 @pytest.mark.parametrize("images,heads,tokens", [(64, 12, 197), (32, 3, 197), (2, 12, 197), (3, 2, 17),
                                                  (1, 1, 1), (2, 3, 32), (2, 3, 65), (1, 2, 256),
-                                                 (4, 1, 200), (2, 2, 150), (5, 3, 97)])
+                                                 (4, 1, 200), (2, 2, 150), (5, 3, 97),
+                                                 # the persistent kernel with a runtime count
+                                                 (48, 12, 200), (48, 12, 193)])
 def test_fused_attention_bf16_is_bitwise_the_launch_sequence(cuvit, oracle, device, images, heads,
                                                              tokens):
     from conftest import bf16_bits
@@ -166,16 +168,18 @@ def test_fused_attention_bf16_is_bitwise_the_launch_sequence(cuvit, oracle, devi
                   f"bf16 fused attention {images}x{heads}x{tokens} differs from the launch sequence")
 
 
+@pytest.mark.parametrize("images,heads", [(2, 3), (64, 12)])
 @pytest.mark.parametrize("stddev", [1.1e-19, 1.0e-10, 30.0])
 def test_fused_attention_bf16_extreme_logits_are_bitwise_the_launch_sequence(cuvit, oracle, device,
-                                                                            stddev):
+                                                                            stddev, images, heads):
     """Logits whose scaled values straddle the smallest normal float (inputs
     of about 1e-19: the GEMM rounds sum / 8, the fused kernel folds the 1/8
     into its exponential), tiny normal ones, and large ones whose
-    exponentials underflow: the same bits as the three launches."""
+    exponentials underflow: the same bits as the three launches, on the
+    per-pair kernel (6 pairs) and on the persistent 197-token instance (768)."""
     from conftest import bf16_bits
 
-    images, heads, tokens = 2, 3, 197
+    tokens = 197
     embed = heads * HEAD_DIM
     qkv = bf16_qkv(oracle, 7500, images * tokens * 3 * embed, device, stddev)
     expected = unfused_bf16(cuvit, qkv, images, heads, tokens, device)
