@@ -37,6 +37,8 @@ vit_tiny_forward  the full batch-32 forward (89 launches: attention fused, posit
 vit_*_forward_bf16 the bf16 model: ViT-Tiny at batch 32 and ViT-Base at batch 64.
 vit_base_b64_bf16 the bf16 twins at ViT-Base/16 batch-64 shapes, cold.
 attention    the fused attention, cold: bf16 at ViT-Base b64, fp32 at ViT-Tiny b32.
+vendor_unfused_bf16 the ViT-Base b64 linear layers as torch linear (hipBLASLt) plus
+             a separate GELU or residual add, for comparison with the fused GEMMs.
 size_sweep   LN, softmax and the gather at ViT-Tiny shapes for batches 32-1024,
              each beside a same-bytes copy.
 cpu_baseline the CPU oracle (a restatement of the reference's CPU loops) on
@@ -526,6 +528,45 @@ def vit_base_bf16(torch, cuvit, device):
     return results
 
 
+def vendor_unfused(torch, device):
+    """The same four ViT-Base b64 linear layers done the unfused way with the
+    vendor library, for comparison with the fused kernels above: torch's
+    linear (hipBLASLt, bf16, its bias epilogue included), then the GELU or the
+    residual add as a separate elementwise pass. Timed as the fused ones (HIP
+    graph of back-to-back launches over two input sets, outputs from the
+    graph's pool). Only the times are used."""
+    rows, embed, hidden = 64 * TOKENS, 768, 3072
+    bf = torch.bfloat16
+    F = torch.nn.functional
+    results = {}
+
+    def time(name, linear, unfused):
+        for f in (linear, unfused):
+            f(0)  # the library's first call outside capture
+        torch.cuda.synchronize()
+        alone = timed_graph(torch, lambda: [linear(i) for i in range(2)], 100) / 2
+        both = timed_graph(torch, lambda: [unfused(i) for i in range(2)], 100) / 2
+        results[name] = {"linear_us": round(alone * 1e3, 3), "unfused_us": round(both * 1e3, 3)}
+
+    a = [torch.randn(rows, embed, device=device).to(bf) for _ in range(2)]
+    w1 = (0.02 * torch.randn(hidden, embed, device=device)).to(bf)
+    b1 = (0.02 * torch.randn(hidden, device=device)).to(bf)
+    time("fc1_gelu_gemm", lambda i: F.linear(a[i], w1, b1), lambda i: F.gelu(F.linear(a[i], w1, b1)))
+    h = [torch.randn(rows, hidden, device=device).to(bf) for _ in range(2)]
+    w2 = (0.02 * torch.randn(embed, hidden, device=device)).to(bf)
+    b2 = (0.02 * torch.randn(embed, device=device)).to(bf)
+    residual = [torch.randn(rows, embed, device=device).to(bf) for _ in range(2)]
+    time("fc2_gemm", lambda i: F.linear(h[i], w2, b2), lambda i: residual[i].add_(F.linear(h[i], w2, b2)))
+    del h
+    w_qkv = (0.02 * torch.randn(3 * embed, embed, device=device)).to(bf)
+    b_qkv = (0.02 * torch.randn(3 * embed, device=device)).to(bf)
+    time("qkv_gemm", lambda i: F.linear(a[i], w_qkv, b_qkv), lambda i: F.linear(a[i], w_qkv, b_qkv))
+    w_p = (0.02 * torch.randn(embed, embed, device=device)).to(bf)
+    time("projection_gemm", lambda i: F.linear(a[i], w_p, b2),
+         lambda i: residual[i].add_(F.linear(a[i], w_p, b2)))
+    return results
+
+
 def attention_block(torch, cuvit, device):
     """The fused attention per launch, cold (rotating pools of the packed QKV
     projection): bf16 at ViT-Base/16 batch 64 (768 (image, head) pairs) and
@@ -849,6 +890,7 @@ def main():
                     "dense peak 2.5 PFLOP/s"}
     line["vit_base_b64_bf16"] = vit_base_bf16(torch, cuvit, device)
     line["attention"] = attention_block(torch, cuvit, device)
+    line["vendor_unfused_bf16"] = vendor_unfused(torch, device)
     line["size_sweep"] = size_sweep(torch, cuvit, device)
     line["preprocess"] = preprocess_block(torch, cuvit, device)
     if not args.no_cpu:

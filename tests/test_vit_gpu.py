@@ -10,6 +10,7 @@ need no oracle (vit_test.cu:134-266).
 from __future__ import annotations
 
 import os
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import pytest
@@ -139,8 +140,9 @@ def test_missing_and_misshaped_weights_are_rejected(cuvit, oracle, device, tmp_p
 
 def test_vit_tiny_batch_32_sequence(cuvit, oracle, device, tmp_path):
     """The full ViT-Tiny/16 layer-kernel sequence at batch 32 (random N(0,0.02)
-    weights, U(-1,1) images, seed 404): image 0 against the CPU VitReference,
-    and every image of the batch bitwise equal to the same image run alone."""
+    weights, U(-1,1) images, seed 404): every image against the CPU
+    VitReference (the oracle's forward runs on host threads, one image each),
+    and images of the batch bitwise equal to the same image run alone."""
     config = tiny_config(cuvit)
     tensors = random_weights(cuvit, oracle, config, 404, small=False)
     path = os.path.join(tmp_path, "tiny.cvw")
@@ -153,9 +155,14 @@ def test_vit_tiny_batch_32_sequence(cuvit, oracle, device, tmp_path):
     together = forward(cuvit, model, images, batch, device)
     assert np.isfinite(together).all()
 
-    expected = oracle.vit_forward(config, [t for _, t in tensors], images[:per_image])
-    require_close(together[0], expected, "ViT-Tiny logits differ from the CPU reference",
-                  1.0e-4, 1.0e-4)
+    weights_list = [t for _, t in tensors]
+    with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as pool:
+        expected = list(pool.map(
+            lambda i: oracle.vit_forward(config, weights_list, images[i * per_image:(i + 1) * per_image]),
+            range(batch)))
+    for i in range(batch):
+        require_close(together[i], expected[i], f"ViT-Tiny logits of image {i} differ from the CPU reference",
+                      1.0e-4, 1.0e-4)
 
     single = cuvit.VisionTransformer(config, weights, 1)
     for i in (0, 13, 31):
