@@ -481,37 +481,40 @@ def vit_base_bf16(torch, cuvit, device):
            lambda i: cuvit.extract_patches(images[i], patches[i], batch, CHANNELS, IMAGE, IMAGE, PATCH),
            len(images))
     del images, patches
-    a = [torch.randn(rows * embed, device=device).to(bf) for _ in range(2)]
+    # The GEMMs' activations rotate through pools larger than 2x the MALL as
+    # the kernels above do (outputs through two buffers), so A comes from HBM
+    # as it does inside the forward, where the previous kernel has just
+    # written it; the weights stay resident, as they would across a batch.
+    a = pool(rows * embed, rows * embed * 2)
     w = (0.02 * torch.randn(hidden * embed, device=device)).to(bf)
     bias = 0.02 * torch.randn(hidden, device=device)
     c = [torch.empty(rows * hidden, device=device, dtype=bf) for _ in range(2)]
     problem = cuvit.gemm_problem(rows, hidden, embed, cuvit.TRANSPOSED)
     problem.epilogue.gelu = 1
     ms = record("fc1_gelu_gemm", 2 * (rows * embed + hidden * embed + rows * hidden),
-                lambda i: cuvit.gemm(a[i], w, bias, c[i], problem), 2)
+                lambda i: cuvit.gemm(a[i], w, bias, c[i % 2], problem), len(a))
     flops = 2.0 * rows * hidden * embed
     results["fc1_gelu_gemm"]["TFLOPs"] = round(flops / (ms * 1e-3) / 1e12, 2)
     results["fc1_gelu_gemm"]["frac_of_bf16_mfma_peak"] = round(flops / (ms * 1e-3) / 2.5e15, 4)
-    del a, c
+    del c
     # FC2 accumulating into the residual stream (M 12608, N 768, K 3072).
-    h = [torch.randn(rows * hidden, device=device).to(bf) for _ in range(2)]
-    residual = [torch.randn(rows * embed, device=device).to(bf) for _ in range(2)]
+    h = pool(rows * hidden, rows * hidden * 2)
+    residual = [torch.randn(rows * embed, device=device).to(bf) for _ in range(len(h))]
     fc2 = cuvit.gemm_problem(rows, embed, hidden, cuvit.TRANSPOSED)
     fc2.epilogue.accumulate = 1
     ms = record("fc2_gemm", 2 * (rows * hidden + embed * hidden + 2 * rows * embed),
-                lambda i: cuvit.gemm(h[i], w, bias, residual[i], fc2), 2)
+                lambda i: cuvit.gemm(h[i], w, bias, residual[i], fc2), len(h))
     results["fc2_gemm"]["TFLOPs"] = round(flops / (ms * 1e-3) / 1e12, 2)
     results["fc2_gemm"]["frac_of_bf16_mfma_peak"] = round(flops / (ms * 1e-3) / 2.5e15, 4)
     del h
     # QKV (M 12608, N 2304, K 768, bias) and the projection accumulating into
     # the residual stream (M 12608, N 768, K 768).
-    x = [torch.randn(rows * embed, device=device).to(bf) for _ in range(2)]
     w_qkv = (0.02 * torch.randn(3 * embed * embed, device=device)).to(bf)
     b_qkv = 0.02 * torch.randn(3 * embed, device=device)
     qkv = [torch.empty(rows * 3 * embed, device=device, dtype=bf) for _ in range(2)]
     p_qkv = cuvit.gemm_problem(rows, 3 * embed, embed, cuvit.TRANSPOSED)
     ms = record("qkv_gemm", 2 * (rows * embed + 3 * embed * embed + 3 * rows * embed),
-                lambda i: cuvit.gemm(x[i], w_qkv, b_qkv, qkv[i], p_qkv), 2)
+                lambda i: cuvit.gemm(a[i], w_qkv, b_qkv, qkv[i % 2], p_qkv), len(a))
     qkv_flops = 2.0 * rows * 3 * embed * embed
     results["qkv_gemm"]["TFLOPs"] = round(qkv_flops / (ms * 1e-3) / 1e12, 2)
     results["qkv_gemm"]["frac_of_bf16_mfma_peak"] = round(qkv_flops / (ms * 1e-3) / 2.5e15, 4)
@@ -520,8 +523,9 @@ def vit_base_bf16(torch, cuvit, device):
     b_proj = b_qkv[:embed]
     p_proj = cuvit.gemm_problem(rows, embed, embed, cuvit.TRANSPOSED)
     p_proj.epilogue.accumulate = 1
+    sets = min(len(a), len(residual))
     ms = record("projection_gemm", 2 * (rows * embed + embed * embed + 2 * rows * embed),
-                lambda i: cuvit.gemm(x[i], w_proj, b_proj, residual[i], p_proj), 2)
+                lambda i: cuvit.gemm(a[i], w_proj, b_proj, residual[i], p_proj), sets)
     proj_flops = 2.0 * rows * embed * embed
     results["projection_gemm"]["TFLOPs"] = round(proj_flops / (ms * 1e-3) / 1e12, 2)
     results["projection_gemm"]["frac_of_bf16_mfma_peak"] = round(proj_flops / (ms * 1e-3) / 2.5e15, 4)
@@ -533,36 +537,44 @@ def vendor_unfused(torch, device):
     vendor library, for comparison with the fused kernels above: torch's
     linear (hipBLASLt, bf16, its bias epilogue included), then the GELU or the
     residual add as a separate elementwise pass. Timed as the fused ones (HIP
-    graph of back-to-back launches over two input sets, outputs from the
-    graph's pool). Only the times are used."""
+    graph of back-to-back launches, activations rotating through the same
+    cold pools, outputs from the graph's pool). Only the times are used."""
     rows, embed, hidden = 64 * TOKENS, 768, 3072
     bf = torch.bfloat16
     F = torch.nn.functional
     results = {}
 
-    def time(name, linear, unfused):
+    def pool(shape):
+        count = shape[0] * shape[1]
+        sets = max(2, -(-POOL_BYTES // (count * 2)))
+        return [torch.randn(shape, device=device).to(bf) for _ in range(sets)]
+
+    def time(name, sets, linear, unfused):
         for f in (linear, unfused):
             f(0)  # the library's first call outside capture
         torch.cuda.synchronize()
-        alone = timed_graph(torch, lambda: [linear(i) for i in range(2)], 100) / 2
-        both = timed_graph(torch, lambda: [unfused(i) for i in range(2)], 100) / 2
+        replays = max(1, 100 // sets)
+        alone = timed_graph(torch, lambda: [linear(i) for i in range(sets)], replays) / sets
+        both = timed_graph(torch, lambda: [unfused(i) for i in range(sets)], replays) / sets
         results[name] = {"linear_us": round(alone * 1e3, 3), "unfused_us": round(both * 1e3, 3)}
 
-    a = [torch.randn(rows, embed, device=device).to(bf) for _ in range(2)]
+    a = pool((rows, embed))
     w1 = (0.02 * torch.randn(hidden, embed, device=device)).to(bf)
     b1 = (0.02 * torch.randn(hidden, device=device)).to(bf)
-    time("fc1_gelu_gemm", lambda i: F.linear(a[i], w1, b1), lambda i: F.gelu(F.linear(a[i], w1, b1)))
-    h = [torch.randn(rows, hidden, device=device).to(bf) for _ in range(2)]
+    time("fc1_gelu_gemm", len(a), lambda i: F.linear(a[i], w1, b1), lambda i: F.gelu(F.linear(a[i], w1, b1)))
+    h = pool((rows, hidden))
     w2 = (0.02 * torch.randn(embed, hidden, device=device)).to(bf)
     b2 = (0.02 * torch.randn(embed, device=device)).to(bf)
-    residual = [torch.randn(rows, embed, device=device).to(bf) for _ in range(2)]
-    time("fc2_gemm", lambda i: F.linear(h[i], w2, b2), lambda i: residual[i].add_(F.linear(h[i], w2, b2)))
+    residual = [torch.randn(rows, embed, device=device).to(bf) for _ in range(len(h))]
+    time("fc2_gemm", len(h), lambda i: F.linear(h[i], w2, b2),
+         lambda i: residual[i].add_(F.linear(h[i], w2, b2)))
     del h
     w_qkv = (0.02 * torch.randn(3 * embed, embed, device=device)).to(bf)
     b_qkv = (0.02 * torch.randn(3 * embed, device=device)).to(bf)
-    time("qkv_gemm", lambda i: F.linear(a[i], w_qkv, b_qkv), lambda i: F.linear(a[i], w_qkv, b_qkv))
+    time("qkv_gemm", len(a), lambda i: F.linear(a[i], w_qkv, b_qkv), lambda i: F.linear(a[i], w_qkv, b_qkv))
     w_p = (0.02 * torch.randn(embed, embed, device=device)).to(bf)
-    time("projection_gemm", lambda i: F.linear(a[i], w_p, b2),
+    sets = min(len(a), len(residual))
+    time("projection_gemm", sets, lambda i: F.linear(a[i], w_p, b2),
          lambda i: residual[i].add_(F.linear(a[i], w_p, b2)))
     return results
 
