@@ -368,10 +368,22 @@ gemm::TileMap balanced_map(const GemmArgs& args, int bm, int bn, int turns) {
 /// height with the fewest rounds x BM (ViT-Base b64: 320 for FC1, 256 for QKV,
 /// 192 for FC2 and the projection). Returns hipErrorNotSupported otherwise.
 hipError_t launch_dma(const std::uint16_t* a, const std::uint16_t* b, const float* bias,
-                      std::uint16_t* c, const GemmArgs& args, hipStream_t stream) {
+                      std::uint16_t* c, const GemmArgs& problem, hipStream_t stream) {
     const int units = compute_units();
+    // A batch whose entries share B and follow one another in A runs as one
+    // problem, each row stored back in its entry: the patch embedding, with
+    // its positional addend (the instance that takes entries).
+    const GemmArgs args = as_one_problem(problem);
+    const bool with_addend = args.addend != nullptr;
+    const bool entries = args.rows_per_entry > 0;
+    // The addend only in the combination the model uses (bias, no alpha, no
+    // GELU, no accumulation), 16-byte runs of it per lane.
+    const bool addend_ok =
+        !with_addend ||
+        (bias != nullptr && args.alpha == 1.0F && !args.gelu && !args.accumulate && aligned16(args.addend) &&
+         args.ld_addend % 4 == 0);
     const bool eligible =
-        args.transposed && args.count == 1 && args.addend == nullptr && args.rows_per_entry == 0 &&
+        args.transposed && args.count == 1 && addend_ok && (!entries || (with_addend && args.stride_c % 8 == 0)) &&
         args.n % 256 == 0 && args.k >= 256 && units % 8 == 0 &&
         vector_operand(a, args.lda, args.k, 0, 0, false) && vector_operand(b, args.ldb, args.k, 0, 0, false) &&
         static_cast<std::int64_t>(320) * args.lda * 2 < gemm::kMaxSpan &&
@@ -383,6 +395,9 @@ hipError_t launch_dma(const std::uint16_t* a, const std::uint16_t* b, const floa
     int bm = 0;
     std::int64_t best = 0;
     for (const int height : {192, 256, 320}) {
+        if (with_addend && height == 320) {
+            continue;  // the addend's registers would spill at 320 rows
+        }
         const std::int64_t tiles = tile_count(args, height, 256);
         const std::int64_t cost = (tiles + units - 1) / units * height;
         if (bm == 0 || cost < best) {
@@ -409,6 +424,13 @@ hipError_t launch_dma(const std::uint16_t* a, const std::uint16_t* b, const floa
     auto pick = [&](auto height) -> hipError_t {
         constexpr int BM = decltype(height)::value;
         constexpr std::size_t kLds = gemm::DmaShape<BM>::kLdsBytes;
+        if (with_addend) {
+            if constexpr (BM == 320) {
+                return hipErrorNotSupported;  // not chosen for an addend (see above)
+            } else {
+                return run(gemm::gemm_dma_kernel<BM, true, false, false, false, true>, kLds);
+            }
+        }
         auto with_flags = [&](auto with_bias, auto with_gelu, auto with_alpha) -> hipError_t {
             constexpr bool kB = decltype(with_bias)::value;
             constexpr bool kG = decltype(with_gelu)::value;

@@ -33,8 +33,8 @@
 //
 // Arithmetic. Each output is the sum gemm_kernel.hpp computes: the same
 // v_mfma_f32_32x32x16_bf16 with B in the first operand, over K rounded up to
-// a multiple of 128 in order, from +0; then alpha * sum, + bias, GELU, + old C
-// (unfused, in that order) and one rounding. So this kernel is bitwise equal
+// a multiple of 128 in order, from +0; then alpha * sum, + bias, + addend,
+// GELU, + old C (unfused, in that order) and one rounding. So this kernel is bitwise equal
 // to the other bf16 kernels and which one runs depends on the shape only.
 #pragma once
 
@@ -110,7 +110,13 @@ template <int BM> struct DmaShape {
     static_assert(kStageBytes >= 8 * 4096, "the consumed stage holds every wavefront's staging");
 };
 
-template <int BM, bool kBias, bool kGelu, bool kAlpha, bool kAccumulate>
+/// @tparam kAddend an [m, n] fp32 term added after the bias (args.addend; the
+///   model's positional add in the patch embedding), its row the output row
+///   within its batch entry; this instance also takes batch entries run as one
+///   problem (args.rows_per_entry > 0), each row stored back in its entry (the
+///   others keep that arithmetic out of their epilogue: FC1's instance, at
+///   256 VGPRs, measured 75 -> 86 us with it).
+template <int BM, bool kBias, bool kGelu, bool kAlpha, bool kAccumulate, bool kAddend = false>
 __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(const std::uint16_t* __restrict__ a,
                                                           const std::uint16_t* __restrict__ b,
                                                           const float* __restrict__ bias,
@@ -221,20 +227,32 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(const std::uint16_t* _
         l.m0 = lds_base + static_cast<unsigned int>((gc & 1) * S::kStageBytes + loader_index * 1024);
         return l;
     };
-    auto load_part = [&](const StageLoads& l, int p) {
+    // Row 32 p + load_row of an operand at k: the lane's byte offset for row
+    // load_row plus p steps of 32 rows (a scalar), added per load. One
+    // offset per row, held across the k loop, took 18 VGPRs: the compiler
+    // spilled, and a reload between a stage's loads waited for all of them.
+    // Past K the offset starts at kOutside, which stays past the descriptor's
+    // range with any step, so the hardware returns zeros; rows past M fall
+    // past it through the row offset itself.
+    const unsigned int a_step = static_cast<unsigned int>(__builtin_amdgcn_readfirstlane(64 * args.lda));
+    const unsigned int b_step = static_cast<unsigned int>(__builtin_amdgcn_readfirstlane(64 * args.ldb));
+    auto issue_loads = [&](const StageLoads& l) {
         if (!l.active) {
             return;
         }
         const bool k_inside = l.k < args.k;
-        if (p < S::kLoadsA) {
-            const unsigned int offset =
-                k_inside ? static_cast<unsigned int>(((load_row + 32 * p) * args.lda + l.k) * 2) : kOutside;
-            load_to_lds(l.m0 + static_cast<unsigned int>(p * 4096), offset, l.ra);
-        } else {
-            const int q = p - S::kLoadsA;
-            const unsigned int offset =
-                k_inside ? static_cast<unsigned int>(((load_row + 32 * q) * args.ldb + l.k) * 2) : kOutside;
-            load_to_lds(l.m0 + static_cast<unsigned int>(BM * 128 + q * 4096), offset, l.rb);
+        const unsigned int a_offset = k_inside ? static_cast<unsigned int>((load_row * args.lda + l.k) * 2) : kOutside;
+        const unsigned int b_offset = k_inside ? static_cast<unsigned int>((load_row * args.ldb + l.k) * 2) : kOutside;
+#pragma unroll
+        for (int p = 0; p < S::kLoads; ++p) {
+            if (p < S::kLoadsA) {
+                load_to_lds(l.m0 + static_cast<unsigned int>(p * 4096), a_offset + static_cast<unsigned int>(p) * a_step,
+                            l.ra);
+            } else {
+                const int q = p - S::kLoadsA;
+                load_to_lds(l.m0 + static_cast<unsigned int>(BM * 128 + q * 4096),
+                            b_offset + static_cast<unsigned int>(q) * b_step, l.rb);
+            }
         }
     };
 
@@ -289,14 +307,26 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(const std::uint16_t* _
         return row0 + wave_m * (BM / 2) + 32 * pair + 8 * k + (lane >> 3);
     };
     const int pair_col = wave_n * 64 + 8 * (lane & 7);
+    // Output row -> its element offset in C (in its batch entry when the
+    // entries run as one problem) and its row within the entry.
+    auto local_row = [&](int row) {
+        return kAddend && args.rows_per_entry > 0 ? row - (row / args.rows_per_entry) * args.rows_per_entry
+                                                  : row;
+    };
+    auto c_offset = [&](int row) -> std::int64_t {
+        if (kAddend && args.rows_per_entry > 0) {
+            const int entry = row / args.rows_per_entry;
+            return entry * args.stride_c + static_cast<std::int64_t>(row - entry * args.rows_per_entry) * args.ldc;
+        }
+        return static_cast<std::int64_t>(row) * args.ldc;
+    };
     auto load_old = [&](int pair, int row0, int col0) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int row = pair_row(pair, row0, k);
             const int col = col0 + pair_col;
-            old_rows[k] = row < args.m && col < args.n
-                              ? load16(c + static_cast<std::int64_t>(row) * args.ldc + col)
-                              : Vec16{{0U, 0U, 0U, 0U}};
+            old_rows[k] = row < args.m && col < args.n ? load16(c + c_offset(row) + col)
+                                                       : Vec16{{0U, 0U, 0U, 0U}};
         }
     };
     auto finish_pair = [&](auto pair_c, unsigned char* staging, int row0, int col0) {
@@ -315,6 +345,23 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(const std::uint16_t* _
         }
         const unsigned char* const bias_slot = lds + S::kBiasOffset;
         const int r = lane & 31;
+        // The addend's four values of each run (j, q) of this lane's row,
+        // all loads in flight before the first is used.
+        Vec16 addend_runs[kAddend ? TN * 4 : 1];
+        if constexpr (kAddend) {
+            const int row = row0 + wave_m * (BM / 2) + 32 * pair + r;
+            const int local = row < args.m ? local_row(row) : 0;
+            const float* const addend_row = args.addend + static_cast<std::int64_t>(local) * args.ld_addend;
+            static_for<TN>([&](auto tile_j) {
+                constexpr int j = decltype(tile_j)::value;
+                static_for<4>([&](auto run) {
+                    constexpr int q = decltype(run)::value;
+                    const int col = col0 + wave_n * 64 + 32 * j + Mma<std::uint16_t>::column(lane, q);
+                    addend_runs[4 * j + q] =
+                        row < args.m && col < args.n ? load16(addend_row + col) : Vec16{{0U, 0U, 0U, 0U}};
+                });
+            });
+        }
         static_for<TN>([&](auto tile_j) {
             constexpr int j = decltype(tile_j)::value;
             static_for<4>([&](auto run) {
@@ -337,6 +384,9 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(const std::uint16_t* _
                     if constexpr (kBias) {
                         x += bias_value[e];
                     }
+                    if constexpr (kAddend) {
+                        x += __uint_as_float(addend_runs[4 * j + q].w[e]);
+                    }
                     v[e] = kGelu ? gelu(x) : x;
                 }
                 if constexpr (kAccumulate) {
@@ -355,18 +405,12 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(const std::uint16_t* _
             const int col = col0 + pair_col;
             const Vec16 v = *reinterpret_cast<const Vec16*>(staged(8 * k + (lane >> 3), lane & 7));
             if (row < args.m && col < args.n) {  // N is a multiple of 8 on this path
-                store16_streaming(c + static_cast<std::int64_t>(row) * args.ldc + col, v);
+                store16_streaming(c + c_offset(row) + col, v);
             }
         }
     };
 
-    auto issue = [&](int g) {
-        const StageLoads l = stage_loads(g);
-#pragma unroll
-        for (int p = 0; p < S::kLoads; ++p) {
-            load_part(l, p);
-        }
-    };
+    auto issue = [&](int g) { issue_loads(stage_loads(g)); };
     if (loader) {
         issue(0);
     }
