@@ -14,19 +14,22 @@
 // (320 x 256 for FC1, 256 x 256 for QKV, 192 x 256 for FC2 and the
 // projection at ViT-Base b64) give one or two nearly full rounds on 256 CUs.
 //
-// Operands. A ring of two 64-deep LDS stages, A rows then B rows of 128
-// bytes. One buffer_load_dwordx4 ... lds moves eight whole 128-byte rows, lane
+// Operands. 64-deep LDS stages, rows of 128 bytes: B in a ring of two, A in
+// a ring of three where LDS allows (192-row tiles: A's loads then go out two
+// stages ahead, which took FC2 from 82 to 72-74 us with A from HBM). One
+// buffer_load_dwordx4 ... lds moves eight whole 128-byte rows, lane
 // l's 16 bytes landing at the instruction's LDS base + 16 l; those loads are
-// issued from inline assembly and waited for by hand (s_waitcnt vmcnt(0)
-// before each stage's barrier), so the compiler neither waits for them early
-// nor drains them at other barriers. Chunk c of stage row r sits in 16-byte
+// issued from inline assembly and waited for by hand (s_waitcnt vmcnt before
+// each stage's barrier, leaving the newest stage's A loads in flight when A
+// runs two ahead), so the compiler neither waits for them early nor drains
+// them at other barriers. Chunk c of stage row r sits in 16-byte
 // slot c ^ ((r >> 1) & 7): conflict-free for the stage writes and for the
 // fragment reads (lane l: row l % 32, chunk 2 kb + l / 32). The last stage of
 // a tile brings the next tile's first stage.
 //
 // Epilogue. Each wavefront finishes its accumulator tiles in pairs (i, 0) and
 // (i, 1), 32 rows by 64 columns: alpha, bias, GELU, + old C, one rounding to
-// bf16, written in the MFMA layout into its own 4 KiB area of the stage just
+// bf16, written in the MFMA layout into its own 4 KiB area of the B slot just
 // consumed, then read back as whole 128-byte rows and stored eight lanes per
 // row (old C comes in the same way). Stores that cover 32 bytes of 32 rows
 // each, straight from the MFMA layout, measured several times slower.
@@ -99,15 +102,23 @@ template <int BM> struct DmaShape {
     static constexpr int kTM = BM / 64;  // MFMA tiles per wavefront: 2 x 4 wavefronts
     static constexpr int kTN = 2;
     static_assert(kBN / 4 == 64, "one wavefront loads the tile's bias, four columns per lane");
-    static constexpr int kStageBytes = (BM + kBN) * 128;  // 64 bf16 of k per row
-    static constexpr int kBiasOffset = 2 * kStageBytes;
+    // A stage is BM rows of A and 256 of B, 64 bf16 of k (128 bytes) per row,
+    // in two rings: B's holds two stages, A's three where LDS allows (192-row
+    // tiles), so that A's loads go out two stages ahead of their use.
+    static constexpr int kASlotBytes = BM * 128;
+    static constexpr int kBSlotBytes = kBN * 128;
+    static constexpr int kASlots = 3 * kASlotBytes + 2 * kBSlotBytes + 1024 + 32 <= 160 * 1024 ? 3 : 2;
+    static constexpr int kAhead = kASlots - 1;  // stages A's loads run ahead
+    static constexpr int kBOffset = kASlots * kASlotBytes;
+    static constexpr int kBiasOffset = kBOffset + 2 * kBSlotBytes;
 
     static constexpr int kLoads = (BM + kBN) / 32;  // load instructions per loading wavefront per stage
     static constexpr int kLoadsA = BM / 32;
     static constexpr int kRoleOffset = kBiasOffset + kBN * 4;  // eight SIMD ids at start-up
     static constexpr int kLdsBytes = kRoleOffset + 8 * 4;
     static_assert(BM % 64 == 0, "whole MFMA tiles per wavefront");
-    static_assert(kStageBytes >= 8 * 4096, "the consumed stage holds every wavefront's staging");
+    static_assert(kBSlotBytes >= 8 * 4096, "a consumed B slot holds every wavefront's staging");
+    static_assert(kLdsBytes <= 160 * 1024, "LDS");
 };
 
 /// @tparam kAddend an [m, n] fp32 term added after the bias (args.addend; the
@@ -203,13 +214,14 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(const std::uint16_t* _
     // row + l / 8, slot l % 8, which holds chunk (l % 8) ^ ((row >> 1) & 7).
     const int load_chunk = (lane & 7) ^ ((4 * (loader_index & 1) + (lane >> 4)) & 7);
     const int load_row = 8 * loader_index + (lane >> 3);
+    // Stage g's A goes to A slot g % kASlots, its B to B slot g % 2.
     struct StageLoads {
-        sgpr4 ra, rb;
+        sgpr4 resource;
         unsigned int m0;
         int k;
         bool active;
     };
-    auto stage_loads = [&](int g) {
+    auto stage_loads = [&](int g, bool operand_a) {
         // Past the last stage the descriptors of the last tile are built and
         // nothing is issued (no branch around them: they stay in SGPRs).
         StageLoads l;
@@ -217,14 +229,19 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(const std::uint16_t* _
         const int gc = l.active ? g : total_stages - 1;
         int row0, col0;
         origin(gc / stages, row0, col0);
-        const int rows_a = min(args.m - row0, BM);
-        const int rows_b = min(args.n - col0, BN);
-        l.ra = scalar_resource(a + static_cast<std::int64_t>(row0) * args.lda,
-                               static_cast<unsigned int>(rows_a * args.lda * 2));
-        l.rb = scalar_resource(b + static_cast<std::int64_t>(col0) * args.ldb,
-                               static_cast<unsigned int>(rows_b * args.ldb * 2));
+        if (operand_a) {
+            const int rows_a = min(args.m - row0, BM);
+            l.resource = scalar_resource(a + static_cast<std::int64_t>(row0) * args.lda,
+                                         static_cast<unsigned int>(rows_a * args.lda * 2));
+            l.m0 = lds_base + static_cast<unsigned int>((gc % S::kASlots) * S::kASlotBytes + loader_index * 1024);
+        } else {
+            const int rows_b = min(args.n - col0, BN);
+            l.resource = scalar_resource(b + static_cast<std::int64_t>(col0) * args.ldb,
+                                         static_cast<unsigned int>(rows_b * args.ldb * 2));
+            l.m0 = lds_base +
+                   static_cast<unsigned int>(S::kBOffset + (gc & 1) * S::kBSlotBytes + loader_index * 1024);
+        }
         l.k = (gc % stages) * 64 + 8 * load_chunk;
-        l.m0 = lds_base + static_cast<unsigned int>((gc & 1) * S::kStageBytes + loader_index * 1024);
         return l;
     };
     // Row 32 p + load_row of an operand at k: the lane's byte offset for row
@@ -236,31 +253,29 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(const std::uint16_t* _
     // past it through the row offset itself.
     const unsigned int a_step = static_cast<unsigned int>(__builtin_amdgcn_readfirstlane(64 * args.lda));
     const unsigned int b_step = static_cast<unsigned int>(__builtin_amdgcn_readfirstlane(64 * args.ldb));
-    auto issue_loads = [&](const StageLoads& l) {
+    auto issue_rows = [&](const StageLoads& l, int ld, unsigned int step, auto count) {
         if (!l.active) {
             return;
         }
-        const bool k_inside = l.k < args.k;
-        const unsigned int a_offset = k_inside ? static_cast<unsigned int>((load_row * args.lda + l.k) * 2) : kOutside;
-        const unsigned int b_offset = k_inside ? static_cast<unsigned int>((load_row * args.ldb + l.k) * 2) : kOutside;
+        const unsigned int offset = l.k < args.k ? static_cast<unsigned int>((load_row * ld + l.k) * 2) : kOutside;
 #pragma unroll
-        for (int p = 0; p < S::kLoads; ++p) {
-            if (p < S::kLoadsA) {
-                load_to_lds(l.m0 + static_cast<unsigned int>(p * 4096), a_offset + static_cast<unsigned int>(p) * a_step,
-                            l.ra);
-            } else {
-                const int q = p - S::kLoadsA;
-                load_to_lds(l.m0 + static_cast<unsigned int>(BM * 128 + q * 4096),
-                            b_offset + static_cast<unsigned int>(q) * b_step, l.rb);
-            }
+        for (int p = 0; p < decltype(count)::value; ++p) {
+            load_to_lds(l.m0 + static_cast<unsigned int>(p * 4096), offset + static_cast<unsigned int>(p) * step,
+                        l.resource);
         }
     };
+    auto issue_a = [&](int g) {
+        issue_rows(stage_loads(g, true), args.lda, a_step, std::integral_constant<int, S::kLoadsA>{});
+    };
+    auto issue_b = [&](int g) {
+        issue_rows(stage_loads(g, false), args.ldb, b_step, std::integral_constant<int, S::kLoads - S::kLoadsA>{});
+    };
 
-    // -- fragments: A tile i at stage row wave_m BM/2 + 32 i + lane % 32, B
-    // tile j at row BM + 64 wave_n + 32 j + lane % 32; k chunk 2 kb + lane / 32.
+    // -- fragments: A tile i at A slot row wave_m BM/2 + 32 i + lane % 32, B
+    // tile j at B slot row 64 wave_n + 32 j + lane % 32; k chunk 2 kb + lane / 32.
     const int swizzle = ((lane & 31) >> 1) & 7;
     const unsigned int a_fragment = static_cast<unsigned int>((wave_m * (BM / 2) + (lane & 31)) * 128);
-    const unsigned int b_fragment = static_cast<unsigned int>((BM + wave_n * 64 + (lane & 31)) * 128);
+    const unsigned int b_fragment = static_cast<unsigned int>((wave_n * 64 + (lane & 31)) * 128);
     unsigned int fragment_column[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
@@ -270,18 +285,19 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(const std::uint16_t* _
     floatx16 acc[TM][TN];
     // The fragments of k-block kb + 1 are read while the MFMAs of kb run (two
     // register sets); scheduling barriers keep that order.
-    auto compute = [&](int slot) {
-        const unsigned char* const base = lds + slot * S::kStageBytes;
+    auto compute = [&](int g) {
+        const unsigned char* const base_a = lds + (g % S::kASlots) * S::kASlotBytes;
+        const unsigned char* const base_b = lds + S::kBOffset + (g & 1) * S::kBSlotBytes;
         Vec16 fa[2][TM];
         Vec16 fb[2][TN];
         auto read = [&](int kb, int set) {
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
-                fa[set][i] = *reinterpret_cast<const Vec16*>(base + a_fragment + i * 4096 + fragment_column[kb]);
+                fa[set][i] = *reinterpret_cast<const Vec16*>(base_a + a_fragment + i * 4096 + fragment_column[kb]);
             }
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
-                fb[set][j] = *reinterpret_cast<const Vec16*>(base + b_fragment + j * 4096 + fragment_column[kb]);
+                fb[set][j] = *reinterpret_cast<const Vec16*>(base_b + b_fragment + j * 4096 + fragment_column[kb]);
             }
         };
         read(0, 0);
@@ -410,9 +426,17 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(const std::uint16_t* _
         }
     };
 
-    auto issue = [&](int g) { issue_loads(stage_loads(g)); };
+    // Stage 0, and A's stages up to kAhead - 1, before the loop. With A two
+    // stages ahead a stage waits for vmcnt(kLoadsA): every load but the
+    // newest stage's A loads has landed.
     if (loader) {
-        issue(0);
+#pragma unroll
+        for (int g = 0; g < S::kAhead; ++g) {
+            issue_a(g);
+            if (g == 0) {
+                issue_b(0);
+            }
+        }
     }
     for (int tile = 0; tile < tiles; ++tile) {
         int row0, col0;
@@ -428,10 +452,22 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(const std::uint16_t* _
             const int g = tile * stages + step;
             // Stage g's loads landed (the loaders wait for their own; a tile's
             // first stage already did, at the barrier before the previous
-            // epilogue), and stage g - 1's slot is free for stage g + 1.
-            stage_barrier(loader && (step > 0 || tile == 0));
+            // epilogue), and stage g - 1's slots are free for the loads below.
+            // The newest kLoadsA loads are stage g + 1's A, issued during stage
+            // g - 1 (or before the loop), unless g + 1 is past the last stage:
+            // then nothing may stay in flight.
+            if (loader && (step > 0 || tile == 0)) {
+                if (S::kAhead == 2 && g + 1 < total_stages) {
+                    static_assert(S::kLoadsA <= 63, "vmcnt");
+                    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(S::kLoadsA) : "memory");
+                } else {
+                    stage_barrier(true);
+                }
+            } else {
+                stage_barrier(false);
+            }
             if (loader) {
-                issue(g + 1);
+                issue_b(g + 1);
                 if (kBias && step == 0 && loader_index == 0) {
                     // the tile's bias (four columns per lane, BN / 4 == 64 lanes),
                     // read by the epilogue after the k loop
@@ -440,14 +476,16 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(const std::uint16_t* _
                     load_to_lds(lds_base + static_cast<unsigned int>(S::kBiasOffset), offset,
                                 scalar_resource(bias, static_cast<unsigned int>(args.n) * 4U));
                 }
+                issue_a(g + S::kAhead);
             }
-            compute(g & 1);
+            compute(g);
         }
         // Every wavefront done with the last stage, the bias and the next
-        // tile's first stage landed: the last stage's slot becomes the
+        // tile's first stages landed: the last stage's B slot becomes the
         // staging areas.
         stage_barrier(true);
-        unsigned char* const staging = lds + ((tile * stages + stages - 1) & 1) * S::kStageBytes + wave * 4096;
+        unsigned char* const staging =
+            lds + S::kBOffset + ((tile * stages + stages - 1) & 1) * S::kBSlotBytes + wave * 4096;
         if constexpr (kAccumulate) {
             load_old(0, row0, col0);
         }
