@@ -115,7 +115,7 @@ WeightFile WeightFile::load(const std::string& path) {
     const auto version = cursor.scalar<std::uint32_t>();
     if (version != kVersion && version != kBFloat16Version) {
         throw std::runtime_error("Weight file " + path + " has version " + std::to_string(version) +
-                                 ", but this build reads versions " + std::to_string(kVersion) +
+                                 ", but this reader takes versions " + std::to_string(kVersion) +
                                  " and " + std::to_string(kBFloat16Version));
     }
     file.version_ = version;
