@@ -456,10 +456,11 @@ hipError_t launch_dma(const std::uint16_t* a, const std::uint16_t* b, const floa
 
 hipError_t gemm_bf16(const std::uint16_t* a, const std::uint16_t* b, const float* bias,
                      std::uint16_t* c, const GemmArgs& args, hipStream_t stream) {
-    // The direct-to-LDS kernel where it applies (ViT-Base b64, A from HBM,
-    // against the kernels below, same bits: FC1 + GELU 101 -> 78 us, QKV 68
-    // -> 52, FC2 accumulating 85 -> 68, the projection 39 -> 27, the patch
-    // embedding 51 -> 29 inside the forward).
+    // The direct-to-LDS kernel where it applies (ViT-Base b64 against the
+    // kernels below, same bits, two input sets: FC1 + GELU 99 -> 87 us, QKV
+    // 61 -> 50, FC2 accumulating 81 -> 67, the projection 38 -> 26; the patch
+    // embedding 51 -> 29 inside the forward. With A from HBM now 78, 52, 68
+    // and 27 us).
     if (const hipError_t dma = launch_dma(a, b, bias, c, args, stream); dma != hipErrorNotSupported) {
         return dma;
     }
