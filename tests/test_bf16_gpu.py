@@ -100,23 +100,26 @@ def test_extract_patches_bf16_staged_strips(cuvit, oracle, device, batch, channe
     require_exact(bf16_bits(y).reshape(expected.shape), expected, "staged bf16 patch gather")
 
 
-@pytest.mark.parametrize("batch,channels,size,patch,offset", [
-    (64, 3, 224, 16, 0),  # ViT-Base/16 batch 64: two 16-byte vectors per patch row
-    (3, 3, 64, 32, 0),    # four vectors per patch row
-    (2, 1, 128, 64, 0),   # eight vectors per patch row, one channel
-    (2, 4, 96, 32, 0),    # four channels, 3 x 3 patches
-    (3, 2, 40, 8, 0),     # one vector per patch row
-    (2, 3, 64, 32, 1),    # images one float off 16-byte alignment (element kernel)
-    (2, 3, 36, 12, 0),    # a patch width that is not a multiple of 8 (element kernel)
+@pytest.mark.parametrize("batch,channels,height,width,patch,offset", [
+    (64, 3, 224, 224, 16, 0),  # ViT-Base/16 batch 64: two 16-byte vectors per patch row
+    (3, 3, 64, 64, 32, 0),     # four vectors per patch row
+    (2, 1, 128, 128, 64, 0),   # eight vectors per patch row, one channel
+    (2, 4, 96, 96, 32, 0),     # four channels, 3 x 3 patches
+    (3, 2, 40, 40, 8, 0),      # one vector per patch row
+    (3, 3, 64, 160, 32, 0),    # non-square: 2 x 5 patches of four vectors a row
+    (2, 2, 192, 64, 64, 0),    # non-square: 3 x 1 patches of eight vectors a row
+    (5, 3, 48, 80, 16, 0),     # non-square: 3 x 5 patches, two vectors a row
+    (2, 3, 64, 64, 32, 1),     # images one float off 16-byte alignment (element kernel)
+    (2, 3, 36, 36, 12, 0),     # a patch width that is not a multiple of 8 (element kernel)
 ])
-def test_extract_patches_f32_to_bf16_one_pass(cuvit, oracle, device, batch, channels, size, patch,
-                                              offset):
+def test_extract_patches_f32_to_bf16_one_pass(cuvit, oracle, device, batch, channels, height, width,
+                                              patch, offset):
     """fp32 images into bf16 patch rows in one pass: bitwise the conversion
     followed by the bf16 gather, and bitwise the oracle's gather of the
     images rounded to nearest-even (ties, signed zeros and infinities
     planted)."""
-    count = batch * channels * size * size
-    images = oracle.generator(515 + size + patch).normal(count, 0.0, 2.0)
+    count = batch * channels * height * width
+    images = oracle.generator(515 + height + width + patch).normal(count, 0.0, 2.0)
     images[::97] = np.float32(1.0 + 2.0 ** -8)    # halfway between two bf16 values: even
     images[5::97] = np.float32(1.0 + 3 * 2.0 ** -8)  # halfway: rounds up to even
     images[7::211] = -0.0
@@ -128,14 +131,14 @@ def test_extract_patches_f32_to_bf16_one_pass(cuvit, oracle, device, batch, chan
         shifted[offset:] = flat
         flat = shifted[offset:]
     one_pass = torch.empty(count, dtype=torch.bfloat16, device=device)
-    cuvit.extract_patches_f32_to_bf16(flat, one_pass, batch, channels, size, size, patch)
+    cuvit.extract_patches_f32_to_bf16(flat, one_pass, batch, channels, height, width, patch)
     converted = torch.empty(count, dtype=torch.bfloat16, device=device)
     cuvit.convert_to_bf16(flat, converted, count)
     two_pass = torch.empty_like(converted)
-    cuvit.extract_patches(converted, two_pass, batch, channels, size, size, patch)
+    cuvit.extract_patches(converted, two_pass, batch, channels, height, width, patch)
     got = bf16_bits(one_pass)
     require_exact(got, bf16_bits(two_pass), "one-pass gather vs conversion then bf16 gather")
-    expected = oracle.round_bf16(oracle.extract_patches(images, batch, channels, size, size, patch))
+    expected = oracle.round_bf16(oracle.extract_patches(images, batch, channels, height, width, patch))
     require_exact(got, expected.reshape(-1), "one-pass gather vs the oracle's rounded gather")
 
 
