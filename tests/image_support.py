@@ -54,4 +54,12 @@ GEOMETRIES = [
     (1000, 20, 64, 0.9, (0.5,) * 3, (0.5,) * 3),
     (257, 255, 384, 1.0, (0.1, 0.2, 0.3), (0.9, -0.5, 2.0)),
     (2, 2, 224, 0.95, (0.5,) * 3, (0.25,) * 3),
+    # the kernel's multiply-and-correct divisions off their guarded range
+    # (division operator): a mean of 1e-30, a standard deviation of 1e-7
+    (64, 48, 32, 0.9, (1e-30,) * 3, (0.3,) * 3),
+    (48, 64, 32, 0.9, (0.4,) * 3, (1e-7, 0.5, 0.5)),
+    # and on it with negative and unrounded standard deviations
+    (33, 47, 24, 0.8, (-0.485, 0.456, 0.0), (-0.229, 3.7, 0.017)),
+    # an even size that is not a multiple of four (the vector kernel)
+    (37, 41, 30, 0.85, IMAGENET_MEAN, IMAGENET_STD),
 ]

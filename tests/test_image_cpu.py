@@ -345,3 +345,89 @@ def test_cli_argument_errors(cuvit, arguments, message):
     result = run_cli(cuvit, *arguments)
     assert result.returncode == 1
     assert result.stderr == f"cu-vit failed: {message}\n"
+
+
+# ------------------------------------------- the device's division forms (host)
+#
+# The preprocessing kernel divides by 255 and by the standard deviation as
+# multiply-and-correct sequences of fused multiply-adds instead of the
+# division operator (preprocess.hip: divide_by_255, divide). Both must round
+# exactly as IEEE division does. The float32 fused multiply-add is emulated
+# exactly here: a * b is exact in float64, and a TwoSum of the float64 sum
+# resolves the one case where rounding it to float32 could differ (a float64
+# sum that lands exactly on a float32 midpoint).
+
+F32, F64 = np.float32, np.float64
+
+
+def _fma32(a, b, c):
+    p = a.astype(F64) * b.astype(F64)
+    c64 = np.asarray(c).astype(F64)
+    s = p + c64
+    bp = s - c64
+    err = (p - bp) + (c64 - (s - bp))
+    r = s.astype(F32)
+    lo = np.where(r.astype(F64) <= s, r, np.nextafter(r, F32(-np.inf)))
+    hi = np.nextafter(lo, F32(np.inf))
+    at_mid = (s == (lo.astype(F64) + hi.astype(F64)) * 0.5) & (err != 0)
+    return np.where(at_mid, np.where(err > 0, hi, lo), r)
+
+
+def _divide_by_255(x):
+    inverse = F32(1.0) / F32(255.0)
+    q = (x.astype(F64) * F64(inverse)).astype(F32)
+    return _fma32(_fma32(np.full_like(x, -255.0), q, x), np.full_like(x, inverse), q)
+
+
+def _divide(a, b, inverse):
+    q0 = (a.astype(F64) * inverse.astype(F64)).astype(F32)
+    q1 = _fma32(_fma32(-b, q0, a), inverse, q0)
+    return _fma32(_fma32(-b, q1, a), inverse, q1)
+
+
+def test_fma_emulation_rounds_midpoints_by_the_exact_sum():
+    """The emulation against exact rational arithmetic on sums built to land
+    on or next to float32 midpoints in float64."""
+    from fractions import Fraction
+
+    rng = np.random.default_rng(11)
+    a = rng.uniform(1.0, 2.0, 2000).astype(F32)
+    b = rng.uniform(1.0, 2.0, 2000).astype(F32)
+    c = (-(a.astype(F64) * b.astype(F64))).astype(F32)  # near cancellation
+    c[::2] = rng.uniform(-4.0, 4.0, 1000).astype(F32)
+    got = _fma32(a, b, c)
+    for i in range(0, 2000, 7):
+        exact = Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i]))
+        down = F32(float(exact))
+        candidates = [np.nextafter(down, F32(-np.inf)), down, np.nextafter(down, F32(np.inf))]
+        best = min(candidates, key=lambda v: (abs(Fraction(float(v)) - exact),
+                                              int(np.array([v]).view(np.uint32)[0]) & 1))
+        assert got[i].view(np.uint32) == best.view(np.uint32), (a[i], b[i], c[i])
+
+
+def test_divide_by_255_rounds_as_ieee_division():
+    """Every integer and half-integer sample, the floats next to them, and
+    one float in 61 over all of [0, 255] (the form was compared with IEEE
+    division for all 1.13e9 floats of that range when it was written)."""
+    top = int(np.array([255.0], F32).view(np.uint32)[0])
+    bits = np.arange(0, top + 1, 61, dtype=np.uint32)
+    grid = np.arange(0, 511, dtype=F64) * 0.5
+    near = np.concatenate([grid.astype(F32), np.nextafter(grid.astype(F32), F32(0)),
+                           np.nextafter(grid.astype(F32), F32(256))])
+    x = np.concatenate([bits.view(F32), near[(near >= 0) & (near <= 255)]]).astype(F32)
+    got = _divide_by_255(x)
+    assert np.array_equal(got.view(np.uint32), (x / F32(255.0)).view(np.uint32))
+
+
+@pytest.mark.parametrize("stddev", [0.5, 0.229, 0.224, 0.225, 1.0, 3.0e-6, 7.0e5])
+def test_corrected_division_rounds_as_ieee_division(stddev):
+    """(sample / 255 - mean) / stddev's second division: numerators of every
+    binade the kernel can meet (2^-61 to 2^21, both signs), each with
+    randomized significands."""
+    rng = np.random.default_rng(int(stddev * 1e6) % 1000 + 5)
+    exponents = rng.integers(-61, 21, 400_000)
+    a = (rng.uniform(1.0, 2.0, exponents.size) * np.exp2(exponents)).astype(F32)
+    a[::2] = -a[::2]
+    b = np.full_like(a, stddev)
+    inverse = np.full_like(a, F32(1.0) / F32(stddev))
+    assert np.array_equal(_divide(a, b, inverse).view(np.uint32), (a / b).view(np.uint32))

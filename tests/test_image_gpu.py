@@ -67,9 +67,9 @@ def test_batch_beyond_one_grid_dimension(cuvit, oracle, device):
         assert np.array_equal(bits(actual[i]), bits(oracle.preprocess(images[i], 2, 1.0)))
 
 
-def test_batch_beyond_one_grid_dimension_four_columns(cuvit, oracle, device):
-    """The same on the four-column kernel: 70,000 images of 2 x 1 pixels at
-    size 4."""
+def test_batch_beyond_one_grid_dimension_vector_kernel(cuvit, oracle, device):
+    """The same on the vector kernel (two output pixels a thread): 70,000
+    images of 2 x 1 pixels at size 4."""
     batch = 70000
     images = np.random.default_rng(8).integers(0, 256, (batch, 1, 2, 3), dtype=np.uint8)
     settings = cuvit.Preprocessing(size=4, crop_fraction=1.0)
@@ -80,8 +80,8 @@ def test_batch_beyond_one_grid_dimension_four_columns(cuvit, oracle, device):
 
 
 def test_unaligned_tensor_takes_the_scalar_kernel(cuvit, oracle, device):
-    """A tensor 4 bytes past a 16-byte boundary cannot take 16-byte stores:
-    the one-pixel-per-thread kernel runs, with the same bits."""
+    """A tensor 4 bytes past a 16-byte boundary does not take the vector
+    kernel's stores: the one-pixel-per-thread kernel runs, with the same bits."""
     pixels = random_pixels(13, 150, 170)
     storage = torch.full((3 * 224 * 224 + 1,), float("nan"), device=device)
     cuvit.preprocess(to_device(pixels[None], device), storage[1:], 1, 170, 150,
