@@ -302,9 +302,10 @@ __global__ __launch_bounds__(kWave) void extract_patches_pair_kernel(
 /// banks. Workgroups are persistent and take kStrips strips per turn; the next
 /// turn's loads are issued before this turn's stores (LDS double-buffered), so
 /// each CU keeps reading while it writes. Measured at ViT-Base batch 64 over
-/// cold buffers, same box: four strips per turn, two workgroups per CU and
-/// non-temporal loads 7.8-7.9 us (plain loads 8.4, three workgroups per CU
-/// 9.2-9.4, one turn per workgroup 8.4-9.5).
+/// cold buffers, one box, strips per turn x workgroups per CU (45.7 KiB of LDS
+/// a workgroup at three strips): 3 x 3 7.7 us, 4 x 2 8.0, 3 x 4 8.4, 1 x 6-8
+/// 8.8, 2 x 2-5 8.7-9.1, 3 x 2 9.5, 5 x 1 10.8; earlier, plain loads instead
+/// of non-temporal ones 8.4 against 7.8-7.9 us at 4 x 2.
 template <int kStrips>
 __global__ __launch_bounds__(448) void extract_patches_staged_bf16_kernel(
     const unsigned char* __restrict__ images, unsigned char* __restrict__ patches, int channels,
@@ -516,10 +517,10 @@ hipError_t dispatch_patches(const void* images, void* patches, int batch, int ch
         }
     }
     if (ElementSize == 2 && aligned16(images) && aligned16(patches) && patch == 16 && width == 224) {
-        constexpr int kStrips = 4;
+        constexpr int kStrips = 3;
         const std::int64_t strips = static_cast<std::int64_t>(batch) * channels * (height / 16);
         const std::int64_t groups = (strips + kStrips - 1) / kStrips;
-        const std::int64_t cap = static_cast<std::int64_t>(compute_units()) * 2;
+        const std::int64_t cap = static_cast<std::int64_t>(compute_units()) * 3;
         const unsigned int grid = static_cast<unsigned int>(groups < cap ? groups : cap);
         extract_patches_staged_bf16_kernel<kStrips><<<grid, 448, 0, stream>>>(
             static_cast<const unsigned char*>(images), static_cast<unsigned char*>(patches), channels,

@@ -81,14 +81,15 @@ def test_extract_patches_bf16_bit_exact(cuvit, oracle, device, batch, size, patc
 
 
 @pytest.mark.parametrize("batch,channels,height", [
-    (1, 3, 224),    # 42 strips: the last group of four holds two
+    (1, 3, 224),    # 42 strips: whole groups of three
+    (1, 1, 224),    # 14 strips: the last group of three holds two
     (5, 1, 96),     # one channel, 6 strips per image, not square
-    (7, 2, 32),     # two strips per plane
+    (7, 2, 32),     # two strips per plane, the last group holds one
     (200, 3, 224),  # 8400 strips: persistent workgroups take several turns
 ])
 def test_extract_patches_bf16_staged_strips(cuvit, oracle, device, batch, channels, height):
     """bf16 images 224 wide in 16 x 16 patches take the LDS-staged strip
-    kernel (four strips a turn, persistent workgroups); every strip count and
+    kernel (three strips a turn, persistent workgroups); every strip count and
     turn count must land bit for bit where the oracle's permutation puts it."""
     width = 224
     bits, _ = bf16_inputs(oracle, 507 + batch, batch * channels * height * width)
