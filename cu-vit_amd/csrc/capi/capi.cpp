@@ -86,10 +86,10 @@ int check_gelu(const void* input, const void* output, std::int64_t count, bool* 
     return ok();
 }
 
-/// Validation shared by the fp32 and bf16 fused attention; @p empty is set
-/// for a launch with nothing to do.
+/// Validation shared by the fp32 and bf16 fused attention (@p element_size
+/// bytes an element); @p empty is set for a launch with nothing to do.
 int check_attention(const void* qkv, const void* context, int images, int heads, int tokens,
-                    int head_dim, bool* empty) {
+                    int head_dim, int element_size, bool* empty) {
     *empty = images == 0 || heads == 0 || tokens == 0 || head_dim == 0;
     if (*empty) {
         return ok();
@@ -109,6 +109,12 @@ int check_attention(const void* qkv, const void* context, int images, int heads,
     }
     if (saturating_product(images, heads) > 65535) {
         return fail(CUVIT_ERROR_LENGTH, "Fused attention takes at most 65535 (image, head) pairs");
+    }
+    // The kernels address an image's rows of the packed projection with
+    // 32-bit byte offsets from the image's first row, inside a buffer range of
+    // 0x7FFFFFF0 bytes.
+    if (static_cast<std::int64_t>(tokens) * 3 * heads * head_dim * element_size > 0x7FFFFFF0) {
+        return fail(CUVIT_ERROR_LENGTH, "Fused attention takes at most 2^31 - 16 bytes of an image's QKV rows");
     }
     return ok();
 }
@@ -587,7 +593,7 @@ int cuvit_attention_supported(int tokens, int head_dim) {
 int cuvit_attention_f32(const float* qkv, float* context, int images, int heads, int tokens,
                         int head_dim, cuvit_stream_t stream) {
     bool empty = false;
-    if (const int s = capi::check_attention(qkv, context, images, heads, tokens, head_dim, &empty);
+    if (const int s = capi::check_attention(qkv, context, images, heads, tokens, head_dim, 4, &empty);
         s != CUVIT_OK || empty) {
         return s;
     }
@@ -599,7 +605,7 @@ int cuvit_attention_f32(const float* qkv, float* context, int images, int heads,
 int cuvit_attention_bf16(const cuvit_bf16* qkv, cuvit_bf16* context, int images, int heads,
                          int tokens, int head_dim, cuvit_stream_t stream) {
     bool empty = false;
-    if (const int s = capi::check_attention(qkv, context, images, heads, tokens, head_dim, &empty);
+    if (const int s = capi::check_attention(qkv, context, images, heads, tokens, head_dim, 2, &empty);
         s != CUVIT_OK || empty) {
         return s;
     }

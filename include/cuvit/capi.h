@@ -138,7 +138,9 @@ int cuvit_broadcast_f32(float* destination, const float* source, int64_t count,
  * logits. qkv is [images, tokens, 3, heads, head_dim] (the QKV projection),
  * context is [images, tokens, heads, head_dim]; both 16-byte aligned.
  * Supports head_dim 64 and up to 256 tokens; other shapes are
- * CUVIT_ERROR_INVALID_ARGUMENT (cuvit_attention_supported tells first). */
+ * CUVIT_ERROR_INVALID_ARGUMENT (cuvit_attention_supported tells first).
+ * More than 65535 (image, head) pairs, or one image's qkv rows past
+ * 0x7FFFFFF0 bytes (the kernels' 32-bit offsets), are CUVIT_ERROR_LENGTH. */
 int cuvit_attention_supported(int tokens, int head_dim);
 int cuvit_attention_f32(const float* qkv, float* context, int images, int heads, int tokens,
                         int head_dim, cuvit_stream_t stream);

@@ -154,7 +154,10 @@ def bf16_qkv(oracle, seed, count, device, stddev=1.0):
                                                  (1, 1, 1), (2, 3, 32), (2, 3, 65), (1, 2, 256),
                                                  (4, 1, 200), (2, 2, 150), (5, 3, 97),
                                                  # the persistent kernel with a runtime count
-                                                 (48, 12, 200), (48, 12, 193)])
+                                                 (48, 12, 200), (48, 12, 193),
+                                                 # and with 1, 2 and 5 key tiles, two or three
+                                                 # pairs per workgroup
+                                                 (520, 1, 20), (130, 4, 64), (44, 12, 150)])
 def test_fused_attention_bf16_is_bitwise_the_launch_sequence(cuvit, oracle, device, images, heads,
                                                              tokens):
     from conftest import bf16_bits

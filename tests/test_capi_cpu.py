@@ -139,6 +139,13 @@ def test_attention_shape_limits(cuvit, lib):
     assert not cuvit.attention_supported(257, 64) and not cuvit.attention_supported(197, 96)
     assert lib.cuvit_attention_f32(FAKE, FAKE, 256, 256, 197, 64, None) == cuvit.ERROR_LENGTH
     assert "65535" in lib.cuvit_last_error().decode()
+    # an image's QKV rows past the kernels' 32-bit offsets: 256 tokens of
+    # 3 x 10923 heads x 64 fp32 values are 65,552 bytes more than 0x7FFFFFF0
+    # (10922 heads would fit); bf16 halves the bytes
+    assert lib.cuvit_attention_f32(FAKE, FAKE, 1, 10923, 256, 64, None) == cuvit.ERROR_LENGTH
+    assert "2^31 - 16 bytes" in lib.cuvit_last_error().decode()
+    assert lib.cuvit_attention_bf16(FAKE, FAKE, 1, 21846, 256, 64, None) == cuvit.ERROR_LENGTH
+    assert "2^31 - 16 bytes" in lib.cuvit_last_error().decode()
 
 
 def gemm_status(cuvit, lib, a=FAKE, b=FAKE, c=FAKE, **fields):
