@@ -311,9 +311,12 @@ template <typename T> void VisionTransformer::load(const WeightFile& file, Store
 
 template <typename T> void VisionTransformer::reserve_activations(Stored<T>& stored) {
     constexpr bool kFloat = std::is_same_v<T, float>;
-    // Attention runs fused (no logits buffer) whenever the shape allows.
+    // Attention runs fused (no logits buffer) whenever the shape allows: the
+    // C ABI's limits on it (pairs, an image's bytes of the QKV projection).
     fused_attention_ = cuvit_attention_supported(config_.token_count(), config_.head_dim()) != 0 &&
-                       static_cast<std::int64_t>(max_batch_) * config_.heads <= 65535;
+                       static_cast<std::int64_t>(max_batch_) * config_.heads <= 65535 &&
+                       static_cast<std::int64_t>(config_.token_count()) * 3 * config_.embed_dim *
+                               static_cast<std::int64_t>(sizeof(T)) <= 0x7FFFFFF0;
 
     const Extent images = max_batch_;
     const Extent embed = config_.embed_dim;
