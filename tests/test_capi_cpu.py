@@ -10,6 +10,7 @@ from __future__ import annotations
 import ctypes
 import os
 import re
+from pathlib import Path
 
 import pytest
 
@@ -19,7 +20,7 @@ FAKE = 0x1000  # a non-null address that is never dereferenced: validation stops
 
 
 def declared_functions():
-    text = open(HEADER).read()
+    text = Path(HEADER).read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(cuvit_[a-z0-9_]+)\s*\(", text)))
 

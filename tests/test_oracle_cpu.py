@@ -15,6 +15,7 @@ from __future__ import annotations
 import json
 import math
 import os
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -336,7 +337,7 @@ def test_generator_reproducible_bounded_and_distributed(oracle):
 def test_generator_matches_committed_streams(oracle):
     """The first values of every seeded stream the configurations use, as
     written by tests/golden/make_golden.py."""
-    streams = json.load(open(os.path.join(GOLDEN, "generator_streams.json")))
+    streams = json.loads(Path(os.path.join(GOLDEN, "generator_streams.json")).read_text())
     for stream in streams:
         g = oracle.generator(stream["seed"])
         if stream["kind"] == "normal":

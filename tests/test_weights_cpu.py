@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import os
 import struct
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -55,7 +56,7 @@ def test_payloads_are_aligned(cuvit, oracle, tmp_path):
     tensors = [("a", np.ones(3, np.float32)), ("bb", np.ones(17, np.float32)),
                ("ccc", np.ones((5, 7), np.float32))]
     _write(cuvit, tensors, path)
-    blob = open(path, "rb").read()
+    blob = Path(path).read_bytes()
     magic, version, count, _ = struct.unpack_from("<4I", blob, 0)
     assert (magic, version, count) == (0x54495643, 1, 3)
     cursor = 16
@@ -108,31 +109,31 @@ def test_corrupt_files_are_rejected(cuvit, tmp_path):
     # version 2; the first version this library does not know is 3
     versioned = str(tmp_path / "version.cvw")
     _write(cuvit, [("weight", np.ones(4, np.float32))], versioned)
-    blob = bytearray(open(versioned, "rb").read())
+    blob = bytearray(Path(versioned).read_bytes())
     struct.pack_into("<I", blob, 4, 3)
-    open(versioned, "wb").write(bytes(blob))
+    Path(versioned).write_bytes(bytes(blob))
     with pytest.raises(cuvit.CuvitError, match="version"):
         cuvit.WeightFile(versioned)
 
     truncated = str(tmp_path / "truncated.cvw")
     _write(cuvit, [("weight", np.ones(64, np.float32))], truncated)
-    blob = open(truncated, "rb").read()
-    open(truncated, "wb").write(blob[:-128])
+    blob = Path(truncated).read_bytes()
+    Path(truncated).write_bytes(blob[:-128])
     with pytest.raises(cuvit.CuvitError):
         cuvit.WeightFile(truncated)
 
     # beyond the reference: a table that ends inside a name, and a byte count
     # that disagrees with the shape
     short = str(tmp_path / "short.cvw")
-    open(short, "wb").write(struct.pack("<4I", 0x54495643, 1, 1, 0) + struct.pack("<I", 50) + b"ab")
+    Path(short).write_bytes(struct.pack("<4I", 0x54495643, 1, 1, 0) + struct.pack("<I", 50) + b"ab")
     with pytest.raises(cuvit.CuvitError, match="name"):
         cuvit.WeightFile(short)
     lying = str(tmp_path / "lying.cvw")
     _write(cuvit, [("w", np.ones(4, np.float32))], lying)
-    blob = bytearray(open(lying, "rb").read())
+    blob = bytearray(Path(lying).read_bytes())
     # entry: name_len(4) + 'w'(1) + type(4) + rank(4) + extent(8) + offset(8) + bytes(8)
     struct.pack_into("<Q", blob, 16 + 4 + 1 + 4 + 4 + 8 + 8, 12)
-    open(lying, "wb").write(bytes(blob))
+    Path(lying).write_bytes(bytes(blob))
     with pytest.raises(cuvit.CuvitError, match="declares"):
         cuvit.WeightFile(lying)
 
@@ -153,7 +154,7 @@ def test_files_interchange_with_the_reference(cuvit, oracle, reference, tmp_path
     theirs = str(tmp_path / "theirs.cvw")
     _write(cuvit, tensors, ours)
     reference.write_weights(theirs, tensors)
-    assert open(ours, "rb").read() == open(theirs, "rb").read(), "the two writers disagree"
+    assert Path(ours).read_bytes() == Path(theirs).read_bytes(), "the two writers disagree"
     loaded = cuvit.WeightFile(theirs)
     for name, values in tensors:
         require_exact(loaded.float_data(name, values.shape), values, f"{name} via our loader")
@@ -164,7 +165,7 @@ def test_files_interchange_with_the_reference(cuvit, oracle, reference, tmp_path
 def test_reference_and_ours_reject_the_same_corruptions(cuvit, reference, tmp_path):
     good = str(tmp_path / "good.cvw")
     _write(cuvit, [("weight", np.ones(64, np.float32))], good)
-    blob = open(good, "rb").read()
+    blob = Path(good).read_bytes()
     cases = {
         "magic": b"XXXX" + blob[4:],
         "version": blob[:4] + struct.pack("<I", 7) + blob[8:],
@@ -174,7 +175,7 @@ def test_reference_and_ours_reject_the_same_corruptions(cuvit, reference, tmp_pa
     }
     for label, content in cases.items():
         path = str(tmp_path / f"{label}.cvw")
-        open(path, "wb").write(content)
+        Path(path).write_bytes(content)
         assert reference.check_weights(path) is not None, f"the reference accepted {label}"
         with pytest.raises(cuvit.CuvitError):
             cuvit.WeightFile(path)
@@ -200,7 +201,7 @@ def test_bf16_round_trip_and_version(cuvit, oracle, tmp_path):
     writer.add("fc.bias", bias)
     writer.add_bf16("specials", specials)
     writer.write(path)
-    blob = open(path, "rb").read()
+    blob = Path(path).read_bytes()
     assert struct.unpack_from("<2I", blob, 0) == (0x54495643, 2)
     loaded = cuvit.WeightFile(path)
     assert loaded.version == 2
@@ -232,7 +233,7 @@ def test_bf16_round_trip_and_version(cuvit, oracle, tmp_path):
 def test_float32_only_files_stay_version_1(cuvit, oracle, tmp_path):
     path = str(tmp_path / "plain.cvw")
     _write(cuvit, _tensors(oracle), path)
-    assert struct.unpack_from("<2I", open(path, "rb").read(), 0) == (0x54495643, 1)
+    assert struct.unpack_from("<2I", Path(path).read_bytes(), 0) == (0x54495643, 1)
     assert cuvit.WeightFile(path).version == 1
 
 
@@ -242,9 +243,9 @@ def test_bf16_type_is_refused_in_a_version_1_file(cuvit, oracle, tmp_path):
     writer = cuvit.WeightWriter()
     writer.add_bf16("w", weight)
     writer.write(path)
-    blob = bytearray(open(path, "rb").read())
+    blob = bytearray(Path(path).read_bytes())
     struct.pack_into("<I", blob, 4, 1)
-    open(path, "wb").write(bytes(blob))
+    Path(path).write_bytes(bytes(blob))
     with pytest.raises(cuvit.CuvitError, match="unsupported data type 2"):
         cuvit.WeightFile(path)
 
